@@ -1,0 +1,210 @@
+"""Benchmark of the MI355X W8A8 arctic-embed-s forward pass (one GPU).
+
+A step is one device forward pass over one token-packed batch of BASELINE
+configs[2] (256 sequences, lengths U{16..512} with [CLS]/[SEP], ids U[1000,30522),
+seed 3) on the seeded synthetic model.  Inputs are resident in HBM
+before the timed region; `value` is embeddings/s over exactly --steps passes.
+
+Also reported: per-kernel device time (HIP events on the workspace stream over
+the timed region) and the roofline of the dominant kernel, ms/seq at 128 tokens
+(configs[0]), and the CPU baseline: the oracle's restatement of the reference's
+scalar path under the reference's embed_batch policy on the host's cores.
+"""
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "snowflake-arctic-embed-s-rust_amd"))
+
+METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
+MODEL_SEED = 0xAE85EED
+PEAK_INT8_TOPS = 5000.0    # MI355X dense int8 MFMA
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def make_batch(n, lo, hi, seed):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, n)
+    return [np.concatenate([[101], rng.integers(1000, 30522, int(L) - 2), [102]]).astype(np.uint16) for L in lens]
+
+
+CONFIGS = {
+    "c1": (lambda: make_batch(1, 128, 128, 1), "c1_1x128"),
+    "c3": (lambda: make_batch(256, 16, 512, 3), "c3_ragged_256x16-512"),
+    "c4": (lambda: make_batch(64, 512, 512, 4), "c4_64x512"),
+    "c5": (lambda: make_batch(8192, 8, 64, 5), "c5_8192x8-64"),
+}
+
+
+def kernel_work(kind, T, B, lens):
+    """Algorithmic work of one launch of `kind` on a packed batch (unit, amount, bound, peak)."""
+    sum_l2 = float(sum(int(L) * int(L) for L in lens))
+    if kind == "gemm_ffn_up":
+        return "TOPS", 2.0 * T * 1536 * 384, "mfma", PEAK_INT8_TOPS
+    if kind == "gemm_ffn_down":
+        return "TOPS", 2.0 * T * 384 * 1536, "mfma", PEAK_INT8_TOPS
+    if kind == "gemm_qkv":
+        return "TOPS", 2.0 * T * 1152 * 384, "mfma", PEAK_INT8_TOPS
+    if kind == "gemm_attn_out":
+        return "TOPS", 2.0 * T * 384 * 384, "mfma", PEAK_INT8_TOPS
+    if kind == "attention":  # QK^T + PV, 12 heads, head_dim 32, f32
+        return "TFLOP/s", 4.0 * 12 * 32 * sum_l2, "mfma", PEAK_FP32_TFLOPS
+    if kind in ("ln1", "ln2"):  # read f32 row, write f32 row + int8 row + scale
+        return "GB/s", T * (384 * 4 * 2 + 384 + 4), "hbm", PEAK_HBM_GBS
+    if kind == "embed_ln":  # gather 2 int8 rows + 2 scales, write f32 row + int8 row + scale
+        return "GB/s", T * (2 * 384 + 8 + 384 * 4 + 384 + 4), "hbm", PEAK_HBM_GBS
+    return None
+
+
+def load_cpu_oracle():
+    """The oracle (scalar restatement of the reference), used only by the cpu_baseline leg."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    return orc
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-sample", type=int, default=32, help="sequences of the workload timed on the CPU")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on exactly one GPU (the forward pass is data-parallel over sequences "
+              "with no cross-GPU exchange; --gpus %d is not supported)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import arctic_embed_amd as ae
+
+    tmp = tempfile.mkdtemp(prefix="ae_bench_")
+    try:
+        ae.write_synthetic_ae8(os.path.join(tmp, "model.ae8"), MODEL_SEED)
+        shutil.copyfile(os.path.join(ROOT, "tests", "golden", "vocab.txt"), os.path.join(tmp, "vocab.txt"))
+        engine = ae.Engine.from_dir(tmp)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+    make, workload = CONFIGS[args.config]
+    seqs = make()
+    lens = [len(s) for s in seqs]
+    B, T = len(seqs), int(sum(lens))
+    ws = engine.workspace(max(T, 512), B)
+    ids_d = torch.from_numpy(np.concatenate(seqs).view(np.int16)).cuda()
+    cu_d = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).cuda()
+    out_d = torch.zeros((B, 384), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.ExternalStream(ws.stream)
+
+    def step():
+        engine.forward_packed_device(ws, ids_d.data_ptr(), cu_d.data_ptr(), B, T, out_d.data_ptr(), ws.stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ws.set_timing(True)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ktimes = ws.kernel_times()
+    ws.set_timing(False)
+    ms_per_step = gpu_ms / args.steps
+    value = B * args.steps / (gpu_ms / 1e3)
+    emb = out_d.cpu().numpy()
+    norms_ok = bool(np.all(np.isfinite(emb)) and np.abs(np.linalg.norm(emb.astype(np.float64), axis=1) - 1).max() < 1e-4)
+
+    # roofline of the dominant kernel kind
+    kernel_ms = {k: v[0] / max(1, args.steps) for k, v in ktimes.items()}
+    dom = max((k for k in kernel_ms if kernel_work(k, T, B, lens)), key=lambda k: kernel_ms[k])
+    unit, amount, bound, peak = kernel_work(dom, T, B, lens)
+    launches = ktimes[dom][1]
+    avg_launch_s = ktimes[dom][0] / 1e3 / max(1, launches)
+    achieved = amount / avg_launch_s / (1e9 if unit == "GB/s" else 1e12)
+    roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 3), "peak": peak,
+                "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+                "avg_launch_us": round(avg_launch_s * 1e6, 2), "algorithmic_per_launch": amount}
+    # the FFN GEMMs' fraction of dense int8 MFMA peak (BASELINE metric, part 2)
+    ffn = {}
+    for k in ("gemm_ffn_up", "gemm_ffn_down"):
+        u, a, _, p = kernel_work(k, T, B, lens)
+        s = ktimes[k][0] / 1e3 / max(1, ktimes[k][1])
+        ffn[k] = round(a / s / 1e12 / p, 4)
+
+    # ms/seq @ 128 tokens (BASELINE metric, part 3): single-sequence latency, device-resident input
+    c1 = make_batch(1, 128, 128, 1)[0]
+    ws1 = engine.workspace(512, 1)
+    ids1 = torch.from_numpy(c1.view(np.int16)).cuda()
+    cu1 = torch.tensor([0, 128], dtype=torch.int32, device="cuda")
+    out1 = torch.zeros((1, 384), dtype=torch.float32, device="cuda")
+    s1 = torch.cuda.ExternalStream(ws1.stream)
+    for _ in range(3):
+        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s1)
+    n1 = 50
+    for _ in range(n1):
+        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream)
+    e1.record(s1)
+    torch.cuda.synchronize()
+    c1_ms = e0.elapsed_time(e1) / n1
+    ws1.close()
+
+    cpu = None
+    if not args.no_cpu:
+        orc = load_cpu_oracle()
+        threads = max(1, min(16, os.cpu_count() or 1))
+        sample = seqs[: args.cpu_sample]
+        m = None
+        tmp = tempfile.mkdtemp(prefix="ae_cpu_")
+        try:
+            ae.write_synthetic_ae8(os.path.join(tmp, "model.ae8"), MODEL_SEED)
+            m = orc.OracleModel(os.path.join(tmp, "model.ae8"))
+        finally:
+            shutil.rmtree(tmp, ignore_errors=True)
+        t0 = time.perf_counter()
+        ref = m.embed_batch_tokens(sample, threads)
+        cpu_s = time.perf_counter() - t0
+        m.close()
+        g = emb[: len(sample)].astype(np.float64)
+        cos = float(((g * ref).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(ref, axis=1))).min())
+        cpu = {"value": round(len(sample) / cpu_s, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
+               "sample": "first %d sequences (%d tokens) of the %s batch, scalar oracle, embed_batch policy"
+                         % (len(sample), sum(len(s) for s in sample), workload),
+               "gpu_vs_cpu_min_cos": round(cos, 9)}
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": workload, "n_seqs": B, "tokens": T, "model": "arctic-embed-s synthetic seed 0xAE85EED"},
+        "tokens_per_s": round(T * args.steps / (gpu_ms / 1e3), 1),
+        "wall_s": round(wall, 4), "outputs_unit_norm": norms_ok,
+        "ffn_int8_mfma_frac": ffn, "ms_per_seq_128": round(c1_ms, 4),
+        "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    ws.close()
+    engine.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,195 @@
+/*
+ * arctic_embed.h -- C ABI of the MI355X-native W8A8 arctic-embed-s engine.
+ *
+ * Drop-in for the public API of mdlockyer/snowflake-arctic-embed-s-rust
+ * (crate `arctic-embed-s-int8`).  Every entry point names the reference item it
+ * replaces (path:line in the reference tree).  Plain C types only: pointers,
+ * sizes, status codes.  Streams are passed as `void*` (a hipStream_t; NULL is
+ * the workspace's own stream for workspace calls, the null stream otherwise).
+ *
+ * Threading: an engine is immutable after open and may be shared by any number
+ * of threads (the reference's `ArcticEmbedS` is shared `&self`).  A workspace
+ * is single-threaded, one per caller thread (the reference's `&mut Workspace`).
+ */
+#ifndef ARCTIC_EMBED_H
+#define ARCTIC_EMBED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- model dimensions: src/quantize.rs:9-18 ----------------------------- */
+#define AE_HIDDEN_SIZE 384
+#define AE_INTERMEDIATE_SIZE 1536
+#define AE_NUM_HEADS 12
+#define AE_HEAD_DIM 32
+#define AE_NUM_LAYERS 12
+#define AE_VOCAB_SIZE 30522
+#define AE_MAX_POSITIONS 512
+
+/* ---- status codes -------------------------------------------------------
+ * The reference returns io::Result / panics; here every failure is a code.
+ *   AE_ERR_NOT_FOUND      io::ErrorKind::NotFound (fs::read, src/quantize.rs:77)
+ *   AE_ERR_INVALID_DATA   bad `.ae8` magic (src/quantize.rs:81-86) or malformed pack
+ *   AE_ERR_EOF            truncated pack (read_exact -> UnexpectedEof)
+ *   AE_ERR_INVALID_ARG    empty ids (the panic at src/model.rs:192), bad sizes, id >= vocab
+ *   AE_ERR_UNSUPPORTED    no usable gfx950 device (src/lib.rs:53-61 analogue)
+ *   AE_ERR_CAPACITY       request exceeds the workspace capacity
+ *   AE_ERR_HIP            a HIP runtime call failed (message in ae_last_error)
+ */
+#define AE_OK 0
+#define AE_ERR_NOT_FOUND (-1)
+#define AE_ERR_INVALID_DATA (-2)
+#define AE_ERR_EOF (-3)
+#define AE_ERR_INVALID_ARG (-4)
+#define AE_ERR_UNSUPPORTED (-5)
+#define AE_ERR_CAPACITY (-6)
+#define AE_ERR_HIP (-7)
+
+typedef struct ae_engine ae_engine;       /* ArcticEmbedS, src/lib.rs:34-38 */
+typedef struct ae_workspace ae_workspace; /* Workspace, src/model.rs:123-173 */
+typedef struct ae_linear ae_linear;       /* PackedLinearInt8, src/gemm.rs:165-181 */
+typedef struct ae_tokenizer ae_tokenizer; /* BertTokenizer, src/tokenizer.rs:26-31 */
+
+/* Human-readable text of the last error raised on the calling thread. */
+const char* ae_last_error(void);
+/* Library version string. */
+const char* ae_version(void);
+
+/* ---- engine ------------------------------------------------------------- */
+/* ArcticEmbedS::from_dir(dir) (src/lib.rs:46-48): reads dir/vocab.txt and
+ * dir/model.ae8 (MODEL_FILE / VOCAB_FILE, src/lib.rs:18-20), uploads the weights
+ * to the current HIP device once.  A NULL dir means default_model_dir()
+ * ($ARCTIC_EMBED_MODEL_DIR or ./model, src/lib.rs:22-31). */
+int ae_engine_open(const char* dir, ae_engine** out);
+/* Same as ae_engine_open with explicit file paths; vocab_path may be NULL for an
+ * ids-only engine (ae_embed_query/_document/_batch then return AE_ERR_INVALID_ARG). */
+int ae_engine_open_files(const char* ae8_path, const char* vocab_path, ae_engine** out);
+void ae_engine_close(ae_engine* e);
+/* ArcticEmbedS::raw_size_bytes = PackedModel::size_bytes (src/lib.rs:65, src/model.rs:87-119),
+ * counted for the device image (weights + scales + biases + smoothing vectors). */
+size_t ae_engine_size_bytes(const ae_engine* e);
+/* QuantizedModelRaw::size_bytes (src/quantize.rs:140-165) of the pack as read. */
+size_t ae_engine_raw_size_bytes(const ae_engine* e);
+/* default_model_dir() (src/lib.rs:26-31) into buf; returns the needed length. */
+size_t ae_default_model_dir(char* buf, size_t cap);
+
+/* ---- workspace ---------------------------------------------------------- */
+/* Workspace::new() (src/model.rs:147-172).  Owns a HIP stream, device activations
+ * sized for max_tokens packed tokens and max_seqs sequences per call, and pinned
+ * host staging.  0 selects the defaults (512 tokens, 64 sequences, as the
+ * reference's Workspace).  Calls larger than the capacity return AE_ERR_CAPACITY. */
+int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, ae_workspace** out);
+void ae_workspace_destroy(ae_workspace* ws);
+/* the workspace's hipStream_t */
+void* ae_workspace_stream(ae_workspace* ws);
+
+/* ---- embedding API ------------------------------------------------------ */
+/* ArcticEmbedS::embed_tokens (src/lib.rs:98-102) -> PackedModel::forward_cls
+ * (src/model.rs:185-513): ids truncated to 512, out = L2-normalized [CLS] f32[384].
+ * n == 0 returns AE_ERR_INVALID_ARG (the reference panics, src/model.rs:192). */
+int ae_embed_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* ids, size_t n, float* out384);
+/* ArcticEmbedS::embed_query / embed_document (src/lib.rs:76-94). */
+int ae_embed_query(const ae_engine* e, ae_workspace* ws, const char* utf8, float* out384);
+int ae_embed_document(const ae_engine* e, ae_workspace* ws, const char* utf8, float* out384);
+/* ArcticEmbedS::embed_batch (src/lib.rs:138-260): out is n*384 floats in input
+ * order; n == 0 is a no-op.  num_threads drives host tokenization only; all
+ * sequences run as token-packed device batches. */
+int ae_embed_batch(const ae_engine* e, ae_workspace* ws, const char* const* texts, size_t n,
+                   int is_query, int num_threads, float* out);
+/* embed_batch over pre-tokenized ids: sequence i is ids[offsets[i] .. offsets[i+1]). */
+int ae_embed_batch_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* ids,
+                          const uint32_t* offsets, size_t n, float* out);
+/* PackedModel::forward_ragged_cls (src/model.rs:521-914) with device-resident
+ * inputs: ids_dev[total_tokens] u16, cu_seqlens_dev[n_seqs+1] i32 (each sequence
+ * 1..512 tokens), out_dev[n_seqs*384] f32.  Asynchronous on `stream`; no host
+ * copies.  Used when the caller keeps token ids in HBM. */
+int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev,
+                             const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                             float* out_dev, void* stream);
+
+/* ---- tokenizer (host only) ---------------------------------------------- */
+/* BertTokenizer::from_vocab_file (src/tokenizer.rs:34-37). */
+int ae_tokenizer_open(const char* vocab_path, ae_tokenizer** out);
+void ae_tokenizer_close(ae_tokenizer* t);
+/* BertTokenizer::encode / encode_query (src/tokenizer.rs:75-89): writes up to cap
+ * ids ([CLS] (+ query prefix) ... [SEP], at most 512) and the count to *n_out. */
+int ae_tokenizer_encode(const ae_tokenizer* t, const char* utf8, int is_query, uint16_t* ids, size_t cap,
+                        size_t* n_out);
+/* BertTokenizer::vocab_size (src/tokenizer.rs:69-71). */
+size_t ae_tokenizer_vocab_size(const ae_tokenizer* t);
+
+/* cosine_similarity (src/lib.rs:265-271): dot product of two f32[384]. */
+float ae_cosine_similarity(const float* a, const float* b);
+
+/* ---- operator level (device pointers, asynchronous on `stream`) ---------- */
+/* PackedLinearInt8::from_raw_row_major (src/gemm.rs:186-246): w_q [n_out,k_in]
+ * row-major int8, w_scale/bias [n_out], inv_smooth [k_in] (host pointers).
+ * Requires n_out % 128 == 0 and k_in % 64 == 0. */
+int ae_linear_create(int n_out, int k_in, const int8_t* w_q, const float* w_scale,
+                     const float* bias, const float* inv_smooth, ae_linear** out);
+void ae_linear_destroy(ae_linear* l);
+/* gemm_int8_fused (src/gemm.rs:630-671):
+ * out[m,n] = fma(f32(sum_k a[m,k]*w[n,k]), a_scale[m]*w_scale[n], bias[n] + res[m,n]).
+ * a_dev [m,k_in] int8 row-major, a_scale_dev [m], res_dev [m,n_out] or NULL. */
+int ae_gemm_w8a8(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
+                 const float* res_dev, float* out_dev, void* stream);
+/* layernorm_smooth_quantize_row (src/simd_math.rs:181-247) over m rows of width 384:
+ * x_dev updated in place, q_dev [m,384] int8, scale_dev [m]. */
+int ae_layernorm_smooth_quantize(int m, float* x_dev, const float* gamma_dev, const float* beta_dev,
+                                 const float* inv_smooth_dev, int8_t* q_dev, float* scale_dev,
+                                 void* stream);
+/* smooth_quantize_row (src/simd_math.rs:501-531) over m rows of width n (n % 64 == 0). */
+int ae_smooth_quantize(int m, int n, const float* x_dev, const float* inv_smooth_dev, int8_t* q_dev,
+                       float* scale_dev, void* stream);
+/* gelu_smooth_quantize_batch (src/simd_math.rs:655-674, 1283-1313) over m rows of
+ * width n (n % 64 == 0): x_dev <- GELU(x)*inv_smooth in place, q_dev, scale_dev. */
+int ae_gelu_smooth_quantize(int m, int n, float* x_dev, const float* inv_smooth_dev, int8_t* q_dev,
+                            float* scale_dev, void* stream);
+/* Segment-bounded multi-head attention of one layer (src/model.rs:663-694):
+ * qkv_dev [T,1152] f32 (Q|K|V, head h at column h*32), cu_seqlens_dev [n_seqs+1],
+ * ctx_dev [T,384] f32. */
+int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
+                        int total_tokens, float* ctx_dev, void* stream);
+
+/* ---- tools and test hooks (no counterpart in the reference) -------------- */
+/* Writes a seeded synthetic model in `.ae8` layout (fp32
+ * N(0,0.02) embeddings stored per-row int8, int8 weights U{-127..127}, scales
+ * 0.05/127*U(0.5,1.5), SmoothQuant 1/U(0.5,2), biases N(0,0.02), LN gamma
+ * 1+N(0,0.05), beta N(0,0.02); layer 11 carries the Q / KV split).  Host only. */
+int ae_write_synthetic_ae8(const char* path, uint64_t seed);
+/* Per-kernel device timing of the workspace's forward passes (hipEvents around
+ * every launch).  Kinds: see AE_KERNEL_* below.  ms_out/counts have AE_KERNEL_KINDS
+ * entries; times cover the passes since timing was enabled and require the
+ * passes to have completed (synchronize first). */
+#define AE_KERNEL_EMBED_LN 0
+#define AE_KERNEL_GEMM_QKV 1
+#define AE_KERNEL_ATTENTION 2
+#define AE_KERNEL_GEMM_ATTN_OUT 3
+#define AE_KERNEL_LN1 4
+#define AE_KERNEL_GEMM_FFN_UP 5
+#define AE_KERNEL_GEMM_FFN_DOWN 6
+#define AE_KERNEL_LN2 7
+#define AE_KERNEL_LAYER11_TAIL 8
+#define AE_KERNEL_KINDS 9
+int ae_workspace_set_timing(ae_workspace* ws, int enabled);
+int ae_workspace_kernel_times(ae_workspace* ws, double* ms_out, int* counts);
+/* The fused GEMM variants of the forward pass, exposed for parity tests:
+ * A given as f32 rows quantized on load with q = round((x*s_k)*(127/rowmax[m]))
+ * (s = smooth_dev, or 1 when NULL) and scale rowmax[m]/127 (rowmax as f32 bits). */
+int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const uint32_t* rowmax_dev,
+                          const float* smooth_dev, const float* res_dev, float* out_dev, void* stream);
+/* int8 A; epilogue g = GELU(out) * g_smooth[n] stored as f32, and
+ * rowmax[m] = max(rowmax[m], max_n |g|) on f32 bits (caller pre-sets rowmax). */
+int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
+                       const float* g_smooth_dev, float* out_dev, uint32_t* rowmax_dev, void* stream);
+/* Device GELU (the reference's scalar_gelu, src/simd_math.rs:15-23) over n floats. */
+int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,338 @@
+"""ctypes binding of libarctic_embed_amd.so (the C ABI in include/arctic_embed.h).
+
+Python mirror of the reference API (mdlockyer/snowflake-arctic-embed-s-rust,
+src/lib.rs): ``ArcticEmbedS.from_dir`` -> ``Engine.from_dir``, ``Workspace``,
+``embed_tokens`` / ``embed_query`` / ``embed_document`` / ``embed_batch``, plus
+the operator-level entry points.  The library is loaded from this directory;
+there is no fallback: a missing library raises ``ImportError``.
+
+Device pointers are plain integers (e.g. ``torch.Tensor.data_ptr()``).
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HIDDEN = 384
+INTER = 1536
+MAX_POS = 512
+VOCAB = 30522
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libarctic_embed_amd.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        "libarctic_embed_amd.so is not built (run __graft_entry__.build() or make -C %s)" % _HERE)
+_lib = ctypes.CDLL(LIB_PATH)
+
+_c = ctypes
+_vp, _sz, _i32, _u64, _f32p = _c.c_void_p, _c.c_size_t, _c.c_int, _c.c_uint64, _c.POINTER(_c.c_float)
+
+_SIGS = {
+    "ae_last_error": (_c.c_char_p, []),
+    "ae_version": (_c.c_char_p, []),
+    "ae_engine_open": (_i32, [_c.c_char_p, _c.POINTER(_vp)]),
+    "ae_engine_open_files": (_i32, [_c.c_char_p, _c.c_char_p, _c.POINTER(_vp)]),
+    "ae_engine_close": (None, [_vp]),
+    "ae_engine_size_bytes": (_sz, [_vp]),
+    "ae_engine_raw_size_bytes": (_sz, [_vp]),
+    "ae_default_model_dir": (_sz, [_c.c_char_p, _sz]),
+    "ae_workspace_create": (_i32, [_vp, _sz, _sz, _c.POINTER(_vp)]),
+    "ae_workspace_destroy": (None, [_vp]),
+    "ae_workspace_stream": (_vp, [_vp]),
+    "ae_embed_tokens": (_i32, [_vp, _vp, _vp, _sz, _vp]),
+    "ae_embed_query": (_i32, [_vp, _vp, _c.c_char_p, _vp]),
+    "ae_embed_document": (_i32, [_vp, _vp, _c.c_char_p, _vp]),
+    "ae_embed_batch": (_i32, [_vp, _vp, _c.POINTER(_c.c_char_p), _sz, _i32, _i32, _vp]),
+    "ae_embed_batch_tokens": (_i32, [_vp, _vp, _vp, _vp, _sz, _vp]),
+    "ae_forward_packed_device": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "ae_cosine_similarity": (_c.c_float, [_vp, _vp]),
+    "ae_linear_create": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _c.POINTER(_vp)]),
+    "ae_linear_destroy": (None, [_vp]),
+    "ae_gemm_w8a8": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ae_layernorm_smooth_quantize": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ae_smooth_quantize": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ae_gelu_smooth_quantize": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ae_attention_varlen": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "ae_write_synthetic_ae8": (_i32, [_c.c_char_p, _u64]),
+    "ae_tokenizer_open": (_i32, [_c.c_char_p, _c.POINTER(_vp)]),
+    "ae_tokenizer_close": (None, [_vp]),
+    "ae_tokenizer_encode": (_i32, [_vp, _c.c_char_p, _i32, _vp, _sz, _c.POINTER(_sz)]),
+    "ae_tokenizer_vocab_size": (_sz, [_vp]),
+    "ae_debug_gelu_map": (_i32, [_vp, _vp, _sz, _vp]),
+    "ae_workspace_set_timing": (_i32, [_vp, _i32]),
+    "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
+    "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ae_debug_gemm_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+# status codes (include/arctic_embed.h)
+AE_OK, AE_ERR_NOT_FOUND, AE_ERR_INVALID_DATA, AE_ERR_EOF = 0, -1, -2, -3
+AE_ERR_INVALID_ARG, AE_ERR_UNSUPPORTED, AE_ERR_CAPACITY, AE_ERR_HIP = -4, -5, -6, -7
+
+
+KERNEL_KINDS = ("embed_ln", "gemm_qkv", "attention", "gemm_attn_out", "ln1", "gemm_ffn_up", "gemm_ffn_down", "ln2",
+                "layer11_tail")
+
+
+class AeError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("ae error %d: %s" % (code, msg))
+        self.code = code
+
+
+def lib():
+    return _lib
+
+
+def _check(rc):
+    if rc != AE_OK:
+        raise AeError(rc, (_lib.ae_last_error() or b"").decode(errors="replace"))
+
+
+def version():
+    return _lib.ae_version().decode()
+
+
+def write_synthetic_ae8(path, seed):
+    """Seeded synthetic model in .ae8 layout."""
+    _check(_lib.ae_write_synthetic_ae8(str(path).encode(), int(seed)))
+
+
+def default_model_dir():
+    n = _lib.ae_default_model_dir(None, 0)
+    buf = ctypes.create_string_buffer(n)
+    _lib.ae_default_model_dir(buf, n)
+    return buf.value.decode()
+
+
+def cosine_similarity(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return float(_lib.ae_cosine_similarity(a.ctypes.data, b.ctypes.data))
+
+
+def _pack_ids(seqs):
+    lens = [len(s) for s in seqs]
+    offsets = np.zeros(len(seqs) + 1, dtype=np.uint32)
+    offsets[1:] = np.cumsum(lens)
+    ids = np.concatenate([np.asarray(s, dtype=np.uint16) for s in seqs]) if seqs else np.zeros(0, np.uint16)
+    return np.ascontiguousarray(ids, dtype=np.uint16), offsets
+
+
+class Tokenizer:
+    """BertTokenizer (src/tokenizer.rs:26-208)."""
+
+    def __init__(self, vocab_path):
+        h = ctypes.c_void_p()
+        _check(_lib.ae_tokenizer_open(str(vocab_path).encode(), ctypes.byref(h)))
+        self._h = h
+
+    def vocab_size(self):
+        return int(_lib.ae_tokenizer_vocab_size(self._h))
+
+    def _enc(self, text, is_query):
+        buf = np.zeros(MAX_POS, dtype=np.uint16)
+        n = ctypes.c_size_t()
+        _check(_lib.ae_tokenizer_encode(self._h, text.encode("utf-8"), 1 if is_query else 0, buf.ctypes.data,
+                                        buf.size, ctypes.byref(n)))
+        return buf[:n.value].copy()
+
+    def encode(self, text):
+        return self._enc(text, False)
+
+    def encode_query(self, text):
+        return self._enc(text, True)
+
+    def close(self):
+        if self._h:
+            _lib.ae_tokenizer_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Engine:
+    """ArcticEmbedS (src/lib.rs:34-72): device-resident weights, shared by threads."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @classmethod
+    def from_dir(cls, path=None):
+        h = ctypes.c_void_p()
+        _check(_lib.ae_engine_open(None if path is None else str(path).encode(), ctypes.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_files(cls, ae8_path, vocab_path=None):
+        h = ctypes.c_void_p()
+        _check(_lib.ae_engine_open_files(str(ae8_path).encode(),
+                                         None if vocab_path is None else str(vocab_path).encode(),
+                                         ctypes.byref(h)))
+        return cls(h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def size_bytes(self):
+        return int(_lib.ae_engine_size_bytes(self._h))
+
+    def raw_size_bytes(self):
+        return int(_lib.ae_engine_raw_size_bytes(self._h))
+
+    def close(self):
+        if self._h:
+            _lib.ae_engine_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def workspace(self, max_tokens=0, max_seqs=0):
+        return Workspace(self, max_tokens, max_seqs)
+
+    # --- embedding API (src/lib.rs:76-260) ---
+    def embed_tokens(self, ws, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint16)
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_tokens(self._h, ws.handle, ids.ctypes.data, ids.size, out.ctypes.data))
+        return out
+
+    def embed_batch_tokens(self, ws, seqs):
+        ids, offsets = _pack_ids(list(seqs))
+        out = np.zeros((len(offsets) - 1, HIDDEN), dtype=np.float32)
+        _check(_lib.ae_embed_batch_tokens(self._h, ws.handle, ids.ctypes.data, offsets.ctypes.data,
+                                          len(offsets) - 1, out.ctypes.data))
+        return out
+
+    def embed_query(self, ws, text):
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_query(self._h, ws.handle, text.encode("utf-8"), out.ctypes.data))
+        return out
+
+    def embed_document(self, ws, text):
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_document(self._h, ws.handle, text.encode("utf-8"), out.ctypes.data))
+        return out
+
+    def embed_batch(self, ws, texts, is_query=False, num_threads=1):
+        n = len(texts)
+        arr = (ctypes.c_char_p * max(n, 1))(*[t.encode("utf-8") for t in texts])
+        out = np.zeros((n, HIDDEN), dtype=np.float32)
+        _check(_lib.ae_embed_batch(self._h, ws.handle, arr, n, 1 if is_query else 0, int(num_threads),
+                                   out.ctypes.data))
+        return out
+
+    def forward_packed_device(self, ws, ids_ptr, cu_ptr, n_seqs, total_tokens, out_ptr, stream=None):
+        _check(_lib.ae_forward_packed_device(self._h, ws.handle, ids_ptr, cu_ptr, int(n_seqs),
+                                             int(total_tokens), out_ptr, stream))
+
+
+class Workspace:
+    """Workspace (src/model.rs:123-173): HIP stream + device activations; one per thread."""
+
+    def __init__(self, engine, max_tokens=0, max_seqs=0):
+        h = ctypes.c_void_p()
+        _check(_lib.ae_workspace_create(engine.handle, int(max_tokens), int(max_seqs), ctypes.byref(h)))
+        self._h = h
+        self._engine = engine
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def stream(self):
+        return _lib.ae_workspace_stream(self._h)
+
+    def set_timing(self, enabled):
+        _check(_lib.ae_workspace_set_timing(self._h, 1 if enabled else 0))
+
+    def kernel_times(self):
+        """{kind: (total_ms, launches)} since timing was enabled (synchronize first)."""
+        ms = np.zeros(len(KERNEL_KINDS), np.float64)
+        cnt = np.zeros(len(KERNEL_KINDS), np.int32)
+        _check(_lib.ae_workspace_kernel_times(self._h, ms.ctypes.data, cnt.ctypes.data))
+        return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(KERNEL_KINDS)}
+
+    def close(self):
+        if self._h:
+            _lib.ae_workspace_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Linear:
+    """PackedLinearInt8 (src/gemm.rs:165-247) on the device."""
+
+    def __init__(self, w_q, w_scale, bias, inv_smooth):
+        w_q = np.ascontiguousarray(w_q, dtype=np.int8)
+        self.n_out, self.k_in = w_q.shape
+        self._keep = [np.ascontiguousarray(x, dtype=np.float32) for x in (w_scale, bias, inv_smooth)]
+        h = ctypes.c_void_p()
+        _check(_lib.ae_linear_create(self.n_out, self.k_in, w_q.ctypes.data, self._keep[0].ctypes.data,
+                                     self._keep[1].ctypes.data, self._keep[2].ctypes.data, ctypes.byref(h)))
+        self._h = h
+
+    def gemm(self, m, a_ptr, a_scale_ptr, res_ptr, out_ptr, stream=None):
+        """gemm_int8_fused (src/gemm.rs:630-671) on device pointers."""
+        _check(_lib.ae_gemm_w8a8(self._h, int(m), a_ptr, a_scale_ptr, res_ptr, out_ptr, stream))
+
+    def gemm_quant_a(self, m, x_ptr, rowmax_ptr, smooth_ptr, res_ptr, out_ptr, stream=None):
+        """GEMM with A quantized on load from f32 rows (the attn_out / FFN-down variant)."""
+        _check(_lib.ae_debug_gemm_quant_a(self._h, int(m), x_ptr, rowmax_ptr, smooth_ptr, res_ptr, out_ptr, stream))
+
+    def gemm_gelu(self, m, a_ptr, a_scale_ptr, g_smooth_ptr, out_ptr, rowmax_ptr, stream=None):
+        """GEMM with the GELU * smooth epilogue and row absmax (the FFN-up variant)."""
+        _check(_lib.ae_debug_gemm_gelu(self._h, int(m), a_ptr, a_scale_ptr, g_smooth_ptr, out_ptr, rowmax_ptr, stream))
+
+    def close(self):
+        if self._h:
+            _lib.ae_linear_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def layernorm_smooth_quantize(m, x_ptr, gamma_ptr, beta_ptr, smooth_ptr, q_ptr, scale_ptr, stream=None):
+    _check(_lib.ae_layernorm_smooth_quantize(int(m), x_ptr, gamma_ptr, beta_ptr, smooth_ptr, q_ptr, scale_ptr,
+                                             stream))
+
+
+def smooth_quantize(m, n, x_ptr, smooth_ptr, q_ptr, scale_ptr, stream=None):
+    _check(_lib.ae_smooth_quantize(int(m), int(n), x_ptr, smooth_ptr, q_ptr, scale_ptr, stream))
+
+
+def gelu_smooth_quantize(m, n, x_ptr, smooth_ptr, q_ptr, scale_ptr, stream=None):
+    _check(_lib.ae_gelu_smooth_quantize(int(m), int(n), x_ptr, smooth_ptr, q_ptr, scale_ptr, stream))
+
+
+def attention_varlen(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None):
+    _check(_lib.ae_attention_varlen(qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), ctx_ptr, stream))
+
+
+def gelu_map(x_ptr, y_ptr, n, stream=None):
+    _check(_lib.ae_debug_gelu_map(x_ptr, y_ptr, int(n), stream))

@@ -1,0 +1,824 @@
+// engine.cpp -- host runtime of the MI355X W8A8 arctic-embed-s engine and the
+// C ABI declared in include/arctic_embed.h.
+//
+// Mirrors the reference's API layer (src/lib.rs) and model driver
+// (src/model.rs): one engine holds the device-resident weights, one workspace
+// per caller thread holds a HIP stream and device activations; a forward pass is
+// one token-packed device batch of any number of sequences.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/arctic_embed.h"
+#include "ae8.hpp"
+#include "kernels.hpp"
+#include "tokenizer.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return fail(AE_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_));       \
+  } while (0)
+
+template <class T>
+int dalloc(T** p, size_t count) {
+  void* v = nullptr;
+  hipError_t e = hipMalloc(&v, count * sizeof(T) > 0 ? count * sizeof(T) : 16);
+  if (e != hipSuccess) return fail(AE_ERR_HIP, std::string("hipMalloc: ") + hipGetErrorString(e));
+  *p = static_cast<T*>(v);
+  return AE_OK;
+}
+
+template <class T>
+int dupload(T** p, const T* src, size_t count) {
+  if (int rc = dalloc(p, count)) return rc;
+  if (count) HIP_TRY(hipMemcpy(*p, src, count * sizeof(T), hipMemcpyHostToDevice));
+  return AE_OK;
+}
+
+int check_device(int* dev_out) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(AE_ERR_UNSUPPORTED, "no HIP device available");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, dev));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(AE_ERR_UNSUPPORTED, std::string("device is ") + prop.gcnArchName + ", this build targets gfx950");
+  *dev_out = dev;
+  return AE_OK;
+}
+
+// [N,K] row-major int8 -> [N/128][K/64][128 rows][64 bytes] (one contiguous
+// 8 KiB tile per (128-column, 64-k) block of the GEMM)
+std::vector<int8_t> swizzle_weights(int n, int k, const int8_t* w) {
+  std::vector<int8_t> out(size_t(n) * k);
+  const int kt_n = k / 64;
+  for (int nt = 0; nt < n / 128; nt++)
+    for (int kt = 0; kt < kt_n; kt++) {
+      int8_t* dst = out.data() + (size_t(nt) * kt_n + kt) * 8192;
+      for (int r = 0; r < 128; r++)
+        std::memcpy(dst + r * 64, w + size_t(nt * 128 + r) * k + kt * 64, 64);
+    }
+  return out;
+}
+
+void free_all(std::vector<void*>& ptrs) {
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  ptrs.clear();
+}
+
+}  // namespace
+
+// PackedLinearInt8 (src/gemm.rs:165-181) on the device
+struct ae_linear {
+  int n = 0, k = 0;
+  int8_t* w = nullptr;  // swizzled
+  float* w_scale = nullptr;
+  float* bias = nullptr;
+  float* inv_smooth = nullptr;
+  bool owns = false;
+  ~ae_linear() {
+    if (owns) {
+      (void)hipFree(w);
+      (void)hipFree(w_scale);
+      (void)hipFree(bias);
+      (void)hipFree(inv_smooth);
+    }
+  }
+};
+
+namespace {
+int make_linear(int n, int k, const int8_t* w_q, const float* w_scale, const float* bias, const float* inv_smooth,
+                ae_linear* l) {
+  if (n <= 0 || k <= 0 || n % 128 || k % 64) return fail(AE_ERR_INVALID_ARG, "linear shape must be n%128==0, k%64==0");
+  l->n = n;
+  l->k = k;
+  l->owns = true;
+  std::vector<int8_t> sw = swizzle_weights(n, k, w_q);
+  if (int rc = dupload(&l->w, sw.data(), sw.size())) return rc;
+  if (int rc = dupload(&l->w_scale, w_scale, size_t(n))) return rc;
+  if (int rc = dupload(&l->bias, bias, size_t(n))) return rc;
+  if (int rc = dupload(&l->inv_smooth, inv_smooth, size_t(k))) return rc;
+  return AE_OK;
+}
+size_t linear_bytes(const ae_linear& l) { return size_t(l.n) * l.k + (size_t(l.n) * 2 + l.k) * 4; }
+}  // namespace
+
+struct DevLayer {
+  ae_linear qkv, q_only, kv_only, attn_out, ffn_inter, ffn_out;
+  float* qkv_smooth = nullptr;  // layer's qkv.inv_smooth (kept for layer 11 where qkv has no weights)
+  float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+};
+
+// ArcticEmbedS (src/lib.rs:34-38): immutable after open
+struct ae_engine {
+  int device = 0;
+  int8_t* word_q = nullptr;
+  float* word_s = nullptr;
+  int8_t* pos_q = nullptr;
+  float* pos_s = nullptr;
+  float* type0 = nullptr;  // pre-dequantized token_type row 0 (src/model.rs:50-54)
+  float* emb_ln_w = nullptr;
+  float* emb_ln_b = nullptr;
+  DevLayer layers[ae::kLayers];
+  std::vector<void*> extra;  // plain device allocations owned by the engine
+  size_t size_bytes = 0, raw_size_bytes = 0;
+  std::unique_ptr<ae::Tokenizer> tokenizer;
+  ~ae_engine() { free_all(extra); }
+};
+
+// Workspace (src/model.rs:123-173): per-thread device scratch + stream
+struct ae_workspace {
+  const ae_engine* e = nullptr;
+  hipStream_t stream = nullptr;
+  int max_tokens = 0, max_seqs = 0;
+  uint16_t* ids = nullptr;
+  int* cu = nullptr;
+  int* tile_start = nullptr;
+  float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
+  int8_t* act_q = nullptr;
+  float* act_scale = nullptr;
+  uint32_t *rowmax_ctx = nullptr, *rowmax_g = nullptr;
+  float *hidden_c = nullptr, *tmp_c = nullptr, *q_c = nullptr, *ctx_c = nullptr, *g_c = nullptr, *out_c = nullptr;
+  int8_t* act_q_c = nullptr;
+  float* act_scale_c = nullptr;
+  uint32_t *rowmax_ctx_c = nullptr, *rowmax_g_c = nullptr;
+  uint16_t* h_ids = nullptr;
+  int* h_cu = nullptr;
+  float* h_out = nullptr;
+  std::vector<void*> dev;
+  // per-kernel timing (ae_workspace_set_timing): event pairs around launches
+  bool timing = false;
+  std::vector<hipEvent_t> ev_pool;
+  std::vector<std::pair<int, int>> ev_marks;  // (kind, index of the start event)
+  size_t ev_used = 0;
+  double kind_ms[AE_KERNEL_KINDS] = {};
+  int kind_count[AE_KERNEL_KINDS] = {};
+  ~ae_workspace() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (hipEvent_t ev : ev_pool) (void)hipEventDestroy(ev);
+    free_all(dev);
+    if (h_ids) (void)hipHostFree(h_ids);
+    if (h_cu) (void)hipHostFree(h_cu);
+    if (h_out) (void)hipHostFree(h_out);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace {
+
+int upload_model(const ae::ModelRaw& m, ae_engine* e) {
+  auto up_i8 = [&](int8_t** p, const std::vector<int8_t>& v) {
+    int rc = dupload(p, v.data(), v.size());
+    e->extra.push_back(*p);
+    return rc;
+  };
+  auto up_f = [&](float** p, const float* v, size_t n) {
+    int rc = dupload(p, v, n);
+    e->extra.push_back(*p);
+    return rc;
+  };
+  int rc;
+  if ((rc = up_i8(&e->word_q, m.word_q)) || (rc = up_f(&e->word_s, m.word_s.data(), m.word_s.size())) ||
+      (rc = up_i8(&e->pos_q, m.pos_q)) || (rc = up_f(&e->pos_s, m.pos_s.data(), m.pos_s.size())) ||
+      (rc = up_f(&e->emb_ln_w, m.emb_ln_w.data(), ae::kHidden)) ||
+      (rc = up_f(&e->emb_ln_b, m.emb_ln_b.data(), ae::kHidden)))
+    return rc;
+  std::vector<float> type0(ae::kHidden);
+  for (int j = 0; j < ae::kHidden; j++) type0[j] = float(m.type_q[j]) * m.type_s[0];
+  if ((rc = up_f(&e->type0, type0.data(), type0.size()))) return rc;
+  size_t bytes = m.word_q.size() + m.pos_q.size() + (m.word_s.size() + m.pos_s.size() + 3 * ae::kHidden) * 4;
+  for (int i = 0; i < ae::kLayers; i++) {
+    const ae::LayerRaw& L = m.layers[i];
+    DevLayer& D = e->layers[i];
+    auto lin = [&](const ae::LinearRaw& r, ae_linear& d) {
+      int c = make_linear(int(r.n_out), int(r.k_in), r.w_q.data(), r.w_scale.data(), r.bias.data(),
+                          r.inv_smooth.data(), &d);
+      bytes += linear_bytes(d);
+      return c;
+    };
+    if (i < ae::kLayers - 1) {
+      if ((rc = lin(L.qkv, D.qkv))) return rc;
+    } else {
+      if ((rc = lin(L.q_only, D.q_only)) || (rc = lin(L.kv_only, D.kv_only))) return rc;
+    }
+    if ((rc = lin(L.attn_out, D.attn_out)) || (rc = lin(L.ffn_inter, D.ffn_inter)) || (rc = lin(L.ffn_out, D.ffn_out)))
+      return rc;
+    if ((rc = up_f(&D.qkv_smooth, L.qkv.inv_smooth.data(), ae::kHidden)) ||
+        (rc = up_f(&D.ln1_w, L.ln1_w.data(), ae::kHidden)) || (rc = up_f(&D.ln1_b, L.ln1_b.data(), ae::kHidden)) ||
+        (rc = up_f(&D.ln2_w, L.ln2_w.data(), ae::kHidden)) || (rc = up_f(&D.ln2_b, L.ln2_b.data(), ae::kHidden)))
+      return rc;
+    bytes += ae::kHidden * 4 * 5;
+  }
+  e->size_bytes = bytes;
+  return AE_OK;
+}
+
+// folds completed event pairs into the per-kind totals
+void drain_timing(ae_workspace* ws) {
+  for (const auto& m : ws->ev_marks) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, ws->ev_pool[m.second], ws->ev_pool[m.second + 1]) == hipSuccess) {
+      ws->kind_ms[m.first] += ms;
+      ws->kind_count[m.first] += 1;
+    }
+  }
+  ws->ev_marks.clear();
+  ws->ev_used = 0;
+}
+
+// RAII event pair around the launches of one kernel kind (no-op unless timing)
+struct KernelTimer {
+  ae_workspace* ws;
+  hipStream_t st;
+  int idx = -1;
+  KernelTimer(ae_workspace* w, hipStream_t s, int kind) : ws(w), st(s) {
+    if (!ws->timing) return;
+    if (ws->ev_used + 2 > ws->ev_pool.size()) return;
+    idx = int(ws->ev_used);
+    ws->ev_used += 2;
+    ws->ev_marks.push_back({kind, idx});
+    (void)hipEventRecord(ws->ev_pool[idx], st);
+  }
+  ~KernelTimer() {
+    if (idx >= 0) (void)hipEventRecord(ws->ev_pool[idx + 1], st);
+  }
+};
+
+// one forward pass over a token-packed batch already resident on the device
+// (PackedModel::forward_ragged_cls, src/model.rs:521-914, without its 64-sequence /
+// 512-token limits).  ids/cu may be the workspace's or the caller's buffers.
+int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int T, float* out, hipStream_t st) {
+  const ae_engine* E = ws->e;
+  using namespace aek;
+  if (ws->timing && ws->ev_used + 2 * 80 > ws->ev_pool.size()) {
+    // pool exhausted by passes not yet folded in: wait for them and fold
+    (void)hipStreamSynchronize(st);
+    drain_timing(ws);
+  }
+  auto gemm = [&](const ae_linear& L, int M, const void* A, int amode, const float* a_scale, const uint32_t* a_rowmax,
+                  const float* a_smooth, const float* res, float* o, int emode, const float* g_smooth,
+                  uint32_t* g_rowmax) {
+    GemmArgs p{};
+    p.M = M;
+    p.N = L.n;
+    p.K = L.k;
+    p.A = A;
+    p.a_scale = a_scale;
+    p.a_rowmax = a_rowmax;
+    p.a_smooth = a_smooth;
+    p.w = L.w;
+    p.w_scale = L.w_scale;
+    p.bias = L.bias;
+    p.res = res;
+    p.out = o;
+    p.g_smooth = g_smooth;
+    p.g_rowmax = g_rowmax;
+    launch_gemm(p, amode, emode, st);
+  };
+  auto ln = [&](const float* src, float* dst, const float* gw, const float* gb, const float* smooth, int8_t* q,
+                float* scale, uint32_t* rowmax_init, int rows) {
+    LnArgs p{};
+    p.T = rows;
+    p.src = src;
+    p.dst = dst;
+    p.gamma = gw;
+    p.beta = gb;
+    p.smooth = smooth;
+    p.q = q;
+    p.scale = scale;
+    p.rowmax_init = rowmax_init;
+    launch_ln_quant(p, kLnSrcF32, st);
+  };
+  {  // embeddings + LayerNorm + SmoothQuant (src/model.rs:549-586)
+    KernelTimer kt(ws, st, AE_KERNEL_EMBED_LN);
+    LnArgs p{};
+    p.T = T;
+    p.ids = ids;
+    p.cu = cu;
+    p.B = B;
+    p.word_q = E->word_q;
+    p.word_s = E->word_s;
+    p.pos_q = E->pos_q;
+    p.pos_s = E->pos_s;
+    p.type0 = E->type0;
+    p.gamma = E->emb_ln_w;
+    p.beta = E->emb_ln_b;
+    p.smooth = E->layers[0].qkv_smooth;
+    p.dst = ws->hidden;
+    p.q = ws->act_q;
+    p.scale = ws->act_scale;
+    p.rowmax_init = ws->rowmax_ctx;
+    launch_ln_quant(p, kLnSrcEmb, st);
+  }
+  const int max_tiles = T / 64 + B + 1;
+  for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
+    const DevLayer& D = E->layers[l];
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_GEMM_QKV);
+      gemm(D.qkv, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->qkv, kEpiF32, nullptr, nullptr);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
+      AttnArgs a{ws->qkv, cu, B, ws->tile_start, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx};
+      launch_attention(a, max_tiles, st);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
+      gemm(D.attn_out, T, ws->ctx, kAF32QSmooth, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
+           kEpiF32, nullptr, nullptr);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_LN1);
+      ln(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale, ws->rowmax_g, T);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
+      gemm(D.ffn_inter, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->g, kEpiGelu,
+           D.ffn_out.inv_smooth, ws->rowmax_g);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
+      gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
+           nullptr);
+    }
+    {
+      KernelTimer kt(ws, st, AE_KERNEL_LN2);
+      ln(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q, ws->act_scale,
+         ws->rowmax_ctx, T);
+    }
+  }
+  // layer 11: [CLS] pruning (src/model.rs:770-913)
+  KernelTimer kt(ws, st, AE_KERNEL_LAYER11_TAIL);
+  const DevLayer& D = E->layers[ae::kLayers - 1];
+  float* kv = ws->qkv;  // [T,768]
+  gemm(D.kv_only, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, kv, kEpiF32, nullptr, nullptr);
+  ClsArgs c{};
+  c.B = B;
+  c.cu = cu;
+  c.hidden = ws->hidden;
+  c.act_q = ws->act_q;
+  c.act_scale = ws->act_scale;
+  c.hidden_c = ws->hidden_c;
+  c.act_q_c = ws->act_q_c;
+  c.act_scale_c = ws->act_scale_c;
+  c.rowmax_init = ws->rowmax_ctx_c;
+  c.q_c = ws->q_c;
+  c.kv = kv;
+  c.ctx_c = ws->ctx_c;
+  c.smooth = D.attn_out.inv_smooth;
+  c.rowmax_ctx_c = ws->rowmax_ctx_c;
+  launch_cls(c, 0, st);
+  gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
+  launch_cls(c, 1, st);
+  gemm(D.attn_out, B, ws->ctx_c, kAF32QSmooth, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth, ws->hidden_c,
+       ws->tmp_c, kEpiF32, nullptr, nullptr);
+  ln(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c, ws->act_scale_c, ws->rowmax_g_c, B);
+  gemm(D.ffn_inter, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->g_c, kEpiGelu,
+       D.ffn_out.inv_smooth, ws->rowmax_g_c);
+  gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->tmp_c, ws->hidden_c, kEpiF32, nullptr,
+       nullptr);
+  launch_final_ln_l2(B, ws->hidden_c, D.ln2_w, D.ln2_b, out, st);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(err));
+  return AE_OK;
+}
+
+// Runs `n` pre-tokenized sequences (already validated and truncated) through as
+// few device batches as the workspace capacity allows.  Sequences are length-
+// sorted so each batch packs similar lengths (length-bucketed packing); results
+// are scattered back to input order.
+int run_sequences(const ae_engine* e, ae_workspace* ws, const std::vector<const uint16_t*>& seqs,
+                  const std::vector<int>& lens, float* out) {
+  const size_t n = seqs.size();
+  std::vector<size_t> order(n);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return lens[a] < lens[b]; });
+  size_t i = 0;
+  while (i < n) {
+    int B = 0, T = 0;
+    size_t j = i;
+    while (j < n && B < ws->max_seqs && T + lens[order[j]] <= ws->max_tokens) {
+      T += lens[order[j]];
+      B++;
+      j++;
+    }
+    if (B == 0) return fail(AE_ERR_CAPACITY, "sequence longer than the workspace token capacity");
+    ws->h_cu[0] = 0;
+    for (int b = 0; b < B; b++) {
+      const size_t s = order[i + b];
+      std::memcpy(ws->h_ids + ws->h_cu[b], seqs[s], size_t(lens[s]) * sizeof(uint16_t));
+      ws->h_cu[b + 1] = ws->h_cu[b] + lens[s];
+    }
+    HIP_TRY(hipMemcpyAsync(ws->ids, ws->h_ids, size_t(T) * sizeof(uint16_t), hipMemcpyHostToDevice, ws->stream));
+    HIP_TRY(hipMemcpyAsync(ws->cu, ws->h_cu, size_t(B + 1) * sizeof(int), hipMemcpyHostToDevice, ws->stream));
+    if (int rc = run_forward(ws, ws->ids, ws->cu, B, T, ws->out_c, ws->stream)) return rc;
+    HIP_TRY(hipMemcpyAsync(ws->h_out, ws->out_c, size_t(B) * ae::kHidden * sizeof(float), hipMemcpyDeviceToHost,
+                           ws->stream));
+    HIP_TRY(hipStreamSynchronize(ws->stream));
+    for (int b = 0; b < B; b++)
+      std::memcpy(out + order[i + b] * ae::kHidden, ws->h_out + size_t(b) * ae::kHidden, ae::kHidden * sizeof(float));
+    i = j;
+  }
+  (void)e;
+  return AE_OK;
+}
+
+int check_ids(const uint16_t* ids, size_t n) {
+  for (size_t i = 0; i < n; i++)
+    if (ids[i] >= ae::kVocab) return fail(AE_ERR_INVALID_ARG, "token id " + std::to_string(ids[i]) + " >= vocab size");
+  return AE_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+extern "C" {
+
+const char* ae_last_error(void) { return g_last_error.c_str(); }
+const char* ae_version(void) { return "arctic-embed-amd 0.1.0 (gfx950)"; }
+
+size_t ae_default_model_dir(char* buf, size_t cap) {
+  const char* env = std::getenv("ARCTIC_EMBED_MODEL_DIR");  // MODEL_DIR_ENV_VAR, src/lib.rs:22
+  std::string d = env ? env : "model";
+  if (buf && cap) {
+    std::strncpy(buf, d.c_str(), cap - 1);
+    buf[cap - 1] = 0;
+  }
+  return d.size() + 1;
+}
+
+int ae_engine_open_files(const char* ae8_path, const char* vocab_path, ae_engine** out) {
+  if (!out || !ae8_path) return fail(AE_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  std::unique_ptr<ae_engine> e(new ae_engine());
+  std::string err;
+  if (vocab_path) {  // BertTokenizer::from_vocab_file (src/tokenizer.rs:34-37) is read first
+    e->tokenizer.reset(new ae::Tokenizer());
+    if (int rc = e->tokenizer->load_vocab_file(vocab_path, err)) return fail(rc, err);
+  }
+  ae::ModelRaw m;
+  if (int rc = ae::load_ae8(ae8_path, m, err)) return fail(rc, err);
+  if (int rc = ae::validate_model(m, err)) return fail(rc, err);
+  e->raw_size_bytes = m.size_bytes();
+  if (int rc = check_device(&e->device)) return rc;
+  if (int rc = upload_model(m, e.get())) return rc;
+  *out = e.release();
+  return AE_OK;
+}
+
+int ae_engine_open(const char* dir, ae_engine** out) {
+  std::string d;
+  if (dir) {
+    d = dir;
+  } else {
+    std::vector<char> buf(ae_default_model_dir(nullptr, 0));
+    ae_default_model_dir(buf.data(), buf.size());
+    d = buf.data();
+  }
+  const std::string vocab = d + "/vocab.txt", pack = d + "/model.ae8";  // VOCAB_FILE / MODEL_FILE
+  return ae_engine_open_files(pack.c_str(), vocab.c_str(), out);
+}
+
+void ae_engine_close(ae_engine* e) {
+  if (e) (void)hipDeviceSynchronize();
+  delete e;
+}
+
+size_t ae_engine_size_bytes(const ae_engine* e) { return e ? e->size_bytes : 0; }
+size_t ae_engine_raw_size_bytes(const ae_engine* e) { return e ? e->raw_size_bytes : 0; }
+
+int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, ae_workspace** out) {
+  if (!e || !out) return fail(AE_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  if (max_tokens == 0) max_tokens = ae::kMaxPos;
+  if (max_seqs == 0) max_seqs = 64;
+  if (max_tokens < size_t(ae::kMaxPos) || max_tokens > (size_t(1) << 26) || max_seqs > max_tokens)
+    return fail(AE_ERR_INVALID_ARG, "workspace needs 512 <= max_tokens <= 2^26 and max_seqs <= max_tokens");
+  HIP_TRY(hipSetDevice(e->device));
+  std::unique_ptr<ae_workspace> ws(new ae_workspace());
+  ws->e = e;
+  ws->max_tokens = int(max_tokens);
+  ws->max_seqs = int(max_seqs);
+  HIP_TRY(hipStreamCreateWithFlags(&ws->stream, hipStreamNonBlocking));
+  const size_t T = max_tokens, B = max_seqs;
+  auto A = [&](auto** p, size_t count) {
+    int rc = dalloc(p, count);
+    ws->dev.push_back(*p);
+    return rc;
+  };
+  int rc;
+  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->tile_start, B + 1)) ||
+      (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
+      (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
+      (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
+      (rc = A(&ws->hidden_c, B * 384)) || (rc = A(&ws->tmp_c, B * 384)) || (rc = A(&ws->q_c, B * 384)) ||
+      (rc = A(&ws->ctx_c, B * 384)) || (rc = A(&ws->g_c, B * 1536)) || (rc = A(&ws->out_c, B * 384)) ||
+      (rc = A(&ws->act_q_c, B * 384)) || (rc = A(&ws->act_scale_c, B)) || (rc = A(&ws->rowmax_ctx_c, B)) ||
+      (rc = A(&ws->rowmax_g_c, B)))
+    return rc;
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_ids), T * sizeof(uint16_t), hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_cu), (B + 1) * sizeof(int), hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_out), B * 384 * sizeof(float), hipHostMallocDefault));
+  *out = ws.release();
+  return AE_OK;
+}
+
+void ae_workspace_destroy(ae_workspace* ws) { delete ws; }
+void* ae_workspace_stream(ae_workspace* ws) { return ws ? reinterpret_cast<void*>(ws->stream) : nullptr; }
+
+int ae_embed_batch_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* ids, const uint32_t* offsets, size_t n,
+                          float* out) {
+  if (!e || !ws || ws->e != e) return fail(AE_ERR_INVALID_ARG, "engine/workspace mismatch");
+  if (n == 0) return AE_OK;  // src/lib.rs:145-147
+  if (!ids || !offsets || !out) return fail(AE_ERR_INVALID_ARG, "null argument");
+  std::vector<const uint16_t*> seqs(n);
+  std::vector<int> lens(n);
+  for (size_t i = 0; i < n; i++) {
+    if (offsets[i + 1] < offsets[i]) return fail(AE_ERR_INVALID_ARG, "offsets must be non-decreasing");
+    const size_t len = offsets[i + 1] - offsets[i];
+    if (len == 0) return fail(AE_ERR_INVALID_ARG, "input_ids must not be empty");  // src/model.rs:192
+    seqs[i] = ids + offsets[i];
+    lens[i] = int(std::min<size_t>(len, ae::kMaxPos));  // src/model.rs:191
+    if (int rc = check_ids(seqs[i], size_t(lens[i]))) return rc;
+  }
+  HIP_TRY(hipSetDevice(e->device));
+  return run_sequences(e, ws, seqs, lens, out);
+}
+
+int ae_embed_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* ids, size_t n, float* out384) {
+  if (n == 0) return fail(AE_ERR_INVALID_ARG, "input_ids must not be empty");
+  uint32_t off[2] = {0, uint32_t(n)};
+  return ae_embed_batch_tokens(e, ws, ids, off, 1, out384);
+}
+
+static int embed_texts(const ae_engine* e, ae_workspace* ws, const char* const* texts, size_t n, bool is_query,
+                       int num_threads, float* out) {
+  if (!e || !ws) return fail(AE_ERR_INVALID_ARG, "null argument");
+  if (!e->tokenizer) return fail(AE_ERR_INVALID_ARG, "engine opened without vocab.txt");
+  if (n == 0) return AE_OK;
+  std::vector<std::vector<uint16_t>> toks;
+  e->tokenizer->encode_batch(texts, n, is_query, num_threads, toks);
+  std::vector<uint16_t> flat;
+  std::vector<uint32_t> offs(n + 1, 0);
+  for (size_t i = 0; i < n; i++) {
+    flat.insert(flat.end(), toks[i].begin(), toks[i].end());
+    offs[i + 1] = uint32_t(flat.size());
+  }
+  return ae_embed_batch_tokens(e, ws, flat.data(), offs.data(), n, out);
+}
+
+int ae_embed_query(const ae_engine* e, ae_workspace* ws, const char* utf8, float* out384) {
+  if (!utf8) return fail(AE_ERR_INVALID_ARG, "null text");
+  return embed_texts(e, ws, &utf8, 1, true, 1, out384);
+}
+
+int ae_embed_document(const ae_engine* e, ae_workspace* ws, const char* utf8, float* out384) {
+  if (!utf8) return fail(AE_ERR_INVALID_ARG, "null text");
+  return embed_texts(e, ws, &utf8, 1, false, 1, out384);
+}
+
+int ae_embed_batch(const ae_engine* e, ae_workspace* ws, const char* const* texts, size_t n, int is_query,
+                   int num_threads, float* out) {
+  if (n && !texts) return fail(AE_ERR_INVALID_ARG, "null texts");
+  return embed_texts(e, ws, texts, n, is_query != 0, num_threads, out);
+}
+
+int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev, const int32_t* cu_seqlens_dev,
+                             int n_seqs, int total_tokens, float* out_dev, void* stream) {
+  if (!e || !ws || ws->e != e) return fail(AE_ERR_INVALID_ARG, "engine/workspace mismatch");
+  if (n_seqs <= 0 || total_tokens < n_seqs || !ids_dev || !cu_seqlens_dev || !out_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad packed batch");
+  if (n_seqs > ws->max_seqs || total_tokens > ws->max_tokens)
+    return fail(AE_ERR_CAPACITY, "packed batch exceeds workspace capacity");
+  hipStream_t st = stream ? as_stream(stream) : ws->stream;
+  return run_forward(ws, ids_dev, cu_seqlens_dev, n_seqs, total_tokens, out_dev, st);
+}
+
+float ae_cosine_similarity(const float* a, const float* b) {  // src/lib.rs:265-271
+  float sum = 0.0f;
+  for (int i = 0; i < ae::kHidden; i++) sum += a[i] * b[i];
+  return sum;
+}
+
+int ae_linear_create(int n_out, int k_in, const int8_t* w_q, const float* w_scale, const float* bias,
+                     const float* inv_smooth, ae_linear** out) {
+  if (!out || !w_q || !w_scale || !bias || !inv_smooth) return fail(AE_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  int dev;
+  if (int rc = check_device(&dev)) return rc;
+  std::unique_ptr<ae_linear> l(new ae_linear());
+  if (int rc = make_linear(n_out, k_in, w_q, w_scale, bias, inv_smooth, l.get())) return rc;
+  *out = l.release();
+  return AE_OK;
+}
+
+void ae_linear_destroy(ae_linear* l) { delete l; }
+
+int ae_gemm_w8a8(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev, const float* res_dev,
+                 float* out_dev, void* stream) {
+  if (!l || !a_dev || !a_scale_dev || !out_dev || m < 0) return fail(AE_ERR_INVALID_ARG, "bad gemm arguments");
+  if (m == 0) return AE_OK;  // src/gemm.rs:639-641
+  aek::GemmArgs p{};
+  p.M = m;
+  p.N = l->n;
+  p.K = l->k;
+  p.A = a_dev;
+  p.a_scale = a_scale_dev;
+  p.w = l->w;
+  p.w_scale = l->w_scale;
+  p.bias = l->bias;
+  p.res = res_dev;
+  p.out = out_dev;
+  aek::launch_gemm(p, aek::kAI8, aek::kEpiF32, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_layernorm_smooth_quantize(int m, float* x_dev, const float* gamma_dev, const float* beta_dev,
+                                 const float* inv_smooth_dev, int8_t* q_dev, float* scale_dev, void* stream) {
+  if (m < 0 || !x_dev || !gamma_dev || !beta_dev || !inv_smooth_dev || !q_dev || !scale_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad layernorm arguments");
+  if (m == 0) return AE_OK;
+  aek::LnArgs p{};
+  p.T = m;
+  p.src = x_dev;
+  p.dst = x_dev;
+  p.gamma = gamma_dev;
+  p.beta = beta_dev;
+  p.smooth = inv_smooth_dev;
+  p.q = q_dev;
+  p.scale = scale_dev;
+  aek::launch_ln_quant(p, aek::kLnSrcF32, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_smooth_quantize(int m, int n, const float* x_dev, const float* inv_smooth_dev, int8_t* q_dev, float* scale_dev,
+                       void* stream) {
+  if (m < 0 || n <= 0 || n % 64 || !x_dev || !inv_smooth_dev || !q_dev || !scale_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad smooth_quantize arguments");
+  if (m == 0) return AE_OK;
+  aek::launch_row_quant(m, n, const_cast<float*>(x_dev), inv_smooth_dev, q_dev, scale_dev, false, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_gelu_smooth_quantize(int m, int n, float* x_dev, const float* inv_smooth_dev, int8_t* q_dev, float* scale_dev,
+                            void* stream) {
+  if (m < 0 || n <= 0 || n % 64 || !x_dev || !inv_smooth_dev || !q_dev || !scale_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad gelu_smooth_quantize arguments");
+  if (m == 0) return AE_OK;
+  aek::launch_row_quant(m, n, x_dev, inv_smooth_dev, q_dev, scale_dev, true, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                        float* ctx_dev, void* stream) {
+  if (!qkv_dev || !cu_seqlens_dev || !ctx_dev || n_seqs < 0 || total_tokens < 0)
+    return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
+  if (n_seqs == 0) return AE_OK;
+  int* tile_start = nullptr;
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&tile_start), size_t(n_seqs + 1) * sizeof(int)));
+  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, tile_start, ctx_dev, nullptr, nullptr};
+  aek::launch_attention(a, total_tokens / 64 + n_seqs + 1, as_stream(stream));
+  hipError_t err = hipStreamSynchronize(as_stream(stream));
+  (void)hipFree(tile_start);
+  if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));
+  return AE_OK;
+}
+
+struct ae_tokenizer {
+  ae::Tokenizer tok;
+};
+
+int ae_tokenizer_open(const char* vocab_path, ae_tokenizer** out) {
+  if (!vocab_path || !out) return fail(AE_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  std::unique_ptr<ae_tokenizer> t(new ae_tokenizer());
+  std::string err;
+  if (int rc = t->tok.load_vocab_file(vocab_path, err)) return fail(rc, err);
+  *out = t.release();
+  return AE_OK;
+}
+
+void ae_tokenizer_close(ae_tokenizer* t) { delete t; }
+
+int ae_tokenizer_encode(const ae_tokenizer* t, const char* utf8, int is_query, uint16_t* ids, size_t cap,
+                        size_t* n_out) {
+  if (!t || !utf8 || !n_out) return fail(AE_ERR_INVALID_ARG, "null argument");
+  std::vector<uint16_t> v;
+  t->tok.encode(utf8, is_query != 0, v);
+  *n_out = v.size();
+  if (v.size() > cap || (!ids && !v.empty())) return fail(AE_ERR_CAPACITY, "id buffer too small");
+  std::memcpy(ids, v.data(), v.size() * sizeof(uint16_t));
+  return AE_OK;
+}
+
+size_t ae_tokenizer_vocab_size(const ae_tokenizer* t) { return t ? t->tok.vocab_size() : 0; }
+
+int ae_write_synthetic_ae8(const char* path, uint64_t seed) {
+  if (!path) return fail(AE_ERR_INVALID_ARG, "null path");
+  std::string err;
+  if (int rc = ae::write_synthetic_ae8(path, seed, err)) return fail(rc, err);
+  return AE_OK;
+}
+
+int ae_workspace_set_timing(ae_workspace* ws, int enabled) {
+  if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
+  HIP_TRY(hipStreamSynchronize(ws->stream));
+  if (enabled && ws->ev_pool.empty()) {
+    ws->ev_pool.resize(4096);
+    for (auto& ev : ws->ev_pool) HIP_TRY(hipEventCreate(&ev));
+  }
+  ws->ev_marks.clear();
+  ws->ev_used = 0;
+  for (int k = 0; k < AE_KERNEL_KINDS; k++) {
+    ws->kind_ms[k] = 0.0;
+    ws->kind_count[k] = 0;
+  }
+  ws->timing = enabled != 0;
+  return AE_OK;
+}
+
+int ae_workspace_kernel_times(ae_workspace* ws, double* ms_out, int* counts) {
+  if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
+  drain_timing(ws);
+  for (int k = 0; k < AE_KERNEL_KINDS; k++) {
+    if (ms_out) ms_out[k] = ws->kind_ms[k];
+    if (counts) counts[k] = ws->kind_count[k];
+  }
+  return AE_OK;
+}
+
+int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const uint32_t* rowmax_dev,
+                          const float* smooth_dev, const float* res_dev, float* out_dev, void* stream) {
+  if (!l || m <= 0 || !x_dev || !rowmax_dev || !out_dev) return fail(AE_ERR_INVALID_ARG, "bad arguments");
+  aek::GemmArgs p{};
+  p.M = m;
+  p.N = l->n;
+  p.K = l->k;
+  p.A = x_dev;
+  p.a_rowmax = rowmax_dev;
+  p.a_smooth = smooth_dev;
+  p.w = l->w;
+  p.w_scale = l->w_scale;
+  p.bias = l->bias;
+  p.res = res_dev;
+  p.out = out_dev;
+  aek::launch_gemm(p, smooth_dev ? aek::kAF32QSmooth : aek::kAF32Q, aek::kEpiF32, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
+                       const float* g_smooth_dev, float* out_dev, uint32_t* rowmax_dev, void* stream) {
+  if (!l || m <= 0 || !a_dev || !a_scale_dev || !g_smooth_dev || !out_dev || !rowmax_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad arguments");
+  aek::GemmArgs p{};
+  p.M = m;
+  p.N = l->n;
+  p.K = l->k;
+  p.A = a_dev;
+  p.a_scale = a_scale_dev;
+  p.w = l->w;
+  p.w_scale = l->w_scale;
+  p.bias = l->bias;
+  p.out = out_dev;
+  p.g_smooth = g_smooth_dev;
+  p.g_rowmax = rowmax_dev;
+  aek::launch_gemm(p, aek::kAI8, aek::kEpiGelu, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+// test hook: exact GELU over n floats on the device (exhaustive parity checks)
+int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream) {
+  aek::launch_gelu_map(x_dev, y_dev, n, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+// kernels.hpp -- host-side launch interface of the gfx950 kernels (kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace aek {
+
+// GEMM A-operand modes
+constexpr int kAI8 = 0;          // int8 rows + per-row scale
+constexpr int kAF32Q = 1;        // f32 rows quantized on load: q = round(x * (127/max))
+constexpr int kAF32QSmooth = 2;  // f32 rows quantized on load: q = round((x * s_k) * (127/max))
+// GEMM epilogues
+constexpr int kEpiF32 = 0;   // out = fma(f32(acc), sa*ws, bias (+res))
+constexpr int kEpiGelu = 1;  // out = GELU(that) * g_smooth[n]; g_rowmax[m] = max |out|
+
+struct GemmArgs {
+  int M, N, K;
+  const void* A;              // int8 [M,K] or f32 [M,K]
+  const float* a_scale;       // kAI8: [M]
+  const uint32_t* a_rowmax;   // kAF32Q*: [M] bits of max_abs (>= 1e-8)
+  const float* a_smooth;      // kAF32QSmooth: inv_smooth [K]
+  const int8_t* w;            // pre-swizzled [N/128][K/64][128][64]
+  const float* w_scale;       // [N]
+  const float* bias;          // [N]
+  const float* res;           // [M,N] or null
+  float* out;                 // [M,N]
+  const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
+  uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
+};
+void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
+
+constexpr int kLnSrcF32 = 0;
+constexpr int kLnSrcEmb = 1;
+struct LnArgs {
+  int T;
+  // kLnSrcEmb
+  const uint16_t* ids;
+  const int* cu;
+  int B;
+  const int8_t* word_q;
+  const float* word_s;
+  const int8_t* pos_q;
+  const float* pos_s;
+  const float* type0;
+  // kLnSrcF32
+  const float* src;
+  const float* gamma;
+  const float* beta;
+  const float* smooth;
+  float* dst;       // LayerNorm output (f32 residual stream), may alias src
+  int8_t* q;        // [T,384]
+  float* scale;     // [T]
+  uint32_t* rowmax_init;   // optional: set to bits(1e-8f) for each row
+  uint32_t* rowmax_init2;  // optional second buffer
+};
+void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st);
+
+void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, float* scale, bool gelu,
+                      hipStream_t st);
+
+struct AttnArgs {
+  const float* qkv;        // [T,1152]
+  const int* cu;           // [B+1]
+  int B;
+  int* tile_start;         // [B+1] scratch
+  float* ctx;              // [T,384]
+  const float* smooth;     // attn_out inv_smooth [384] or null
+  uint32_t* rowmax;        // [T] or null
+};
+void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st);
+
+struct ClsArgs {
+  int B;
+  const int* cu;
+  const float* hidden;     // [T,384]
+  const int8_t* act_q;     // [T,384]
+  const float* act_scale;  // [T]
+  float* hidden_c;         // [B,384]
+  int8_t* act_q_c;         // [B,384]
+  float* act_scale_c;      // [B]
+  uint32_t* rowmax_init;   // [B] ctx row-absmax buffer to reset
+  const float* q_c;        // [B,384]
+  const float* kv;         // [T,768]
+  float* ctx_c;            // [B,384]
+  const float* smooth;     // attn_out inv_smooth
+  uint32_t* rowmax_ctx_c;  // [B]
+};
+void launch_cls(const ClsArgs& p, int stage, hipStream_t st);
+void launch_final_ln_l2(int B, const float* src, const float* gamma, const float* beta, float* out, hipStream_t st);
+void launch_fill_u32(uint32_t* dst, int n, uint32_t v, hipStream_t st);
+void launch_gelu_map(const float* x, float* y, size_t n, hipStream_t st);
+
+}  // namespace aek

@@ -1,0 +1,107 @@
+"""CPU-side checks of the product library: it loads, exports every symbol the C
+header declares, reads/validates `.ae8` packs with the reference's error
+semantics, and its tokenizer reproduces the reference's id vectors."""
+import json
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import arctic_embed_amd as ae
+from conftest import GOLDEN, ROOT
+
+HEADER = os.path.join(ROOT, "include", "arctic_embed.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ae_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 30
+    out = subprocess.run(["nm", "-D", "--defined-only", ae.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (ae_[a-z0-9_]+)", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    for n in names:  # resolvable through the dynamic loader as well
+        getattr(ae.lib(), n)
+
+
+def test_version_and_default_dir(monkeypatch):
+    assert "gfx950" in ae.version()
+    monkeypatch.setenv("ARCTIC_EMBED_MODEL_DIR", "/some/dir")
+    assert ae.default_model_dir() == "/some/dir"
+    monkeypatch.delenv("ARCTIC_EMBED_MODEL_DIR")
+    assert ae.default_model_dir() == "model"
+
+
+def test_cosine_similarity():
+    rng = np.random.default_rng(0)
+    a = rng.normal(size=384).astype(np.float32)
+    b = rng.normal(size=384).astype(np.float32)
+    s = np.float32(0)
+    for i in range(384):  # sequential f32 dot (src/lib.rs:265-271)
+        s = np.float32(s + a[i] * b[i])
+    assert ae.cosine_similarity(a, b) == s
+
+
+def _open_code(ae8, vocab):
+    try:
+        e = ae.Engine.from_files(ae8, vocab)
+    except ae.AeError as err:
+        return err.code
+    e.close()
+    return ae.AE_OK
+
+
+def test_pack_errors_follow_reference(tmp_path, model_dir):
+    data = open(str(model_dir / "model.ae8"), "rb").read()
+    vocab = str(model_dir / "vocab.txt")
+    assert _open_code(str(tmp_path / "none.ae8"), vocab) == ae.AE_ERR_NOT_FOUND
+    assert _open_code(str(model_dir / "model.ae8"), str(tmp_path / "none.txt")) == ae.AE_ERR_NOT_FOUND
+    bad = tmp_path / "bad.ae8"
+    bad.write_bytes(b"ARCTIC9\x01" + data[8:])
+    assert _open_code(str(bad), vocab) == ae.AE_ERR_INVALID_DATA
+    for cut in (3, 8, 100, len(data) - 10):
+        t = tmp_path / ("t%d.ae8" % cut)
+        t.write_bytes(data[:cut])
+        assert _open_code(str(t), vocab) == ae.AE_ERR_EOF, cut
+
+
+def test_valid_pack_without_gpu_reports_unsupported(model_dir):
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert _open_code(str(model_dir / "model.ae8"), str(model_dir / "vocab.txt")) == ae.AE_ERR_UNSUPPORTED
+
+
+def test_tokenizer_reference_vectors():
+    tok = ae.Tokenizer(os.path.join(GOLDEN, "vocab.txt"))
+    assert tok.vocab_size() == 30522
+    d = json.load(open(os.path.join(GOLDEN, "tokenizer_vectors.json"), encoding="utf-8"))
+    assert len(d["short"]) == 12 and len(d["long"]) == 7
+    for r in d["short"]:  # tests/accuracy_test.rs:86-96
+        ids = tok.encode_query(r["raw_text"]) if r["kind"] == "query" else tok.encode(r["raw_text"])
+        assert list(ids) == r["ids"], r["raw_text"]
+    for r in d["long"]:  # examples/dump_ids.rs: BertTokenizer::encode per line
+        assert list(tok.encode(r["text"])) == r["ids"], r["name"]
+
+
+def test_tokenizer_edge_cases():
+    tok = ae.Tokenizer(os.path.join(GOLDEN, "vocab.txt"))
+    assert list(tok.encode("")) == [101, 102]
+    assert list(tok.encode("\x00�\x07")) == [101, 102]     # removed by the normalizer
+    assert list(tok.encode("HELLO")) == list(tok.encode("hello"))  # lowercase
+    assert list(tok.encode("café")) == list(tok.encode("cafe"))  # accent stripping
+    assert list(tok.encode("café")) == list(tok.encode("cafe"))  # combining mark dropped
+    long = tok.encode("word " * 1000)
+    assert len(long) == 512 and long[0] == 101 and long[-1] == 102
+    q = tok.encode_query("x")
+    assert len(q) > 3 and q[0] == 101 and q[-1] == 102
+    assert list(tok.encode("a" * 101)) == [101, 100, 102]  # > 100 chars -> [UNK]
+    assert list(tok.encode("中文"))[1:-1] == list(tok.encode("中 文"))[1:-1]

@@ -1,0 +1,147 @@
+"""End-to-end parity of the device forward pass (through the C ABI) against the
+oracle's restatement of forward_cls / embed_batch.
+
+Bar: per embedding cosine >= 0.99999 and max |diff| <= 1e-4
+against the oracle.  Attention is f32 in a different summation order, so a rare
+int8 activation can flip by one step; everything else is bit-exact on identical
+inputs (see test_gpu_kernels.py).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import arctic_embed_amd as ae
+from conftest import GOLDEN, c1_ids, ragged_batch
+
+pytestmark = pytest.mark.gpu
+COS_MIN, MAXABS = 0.99999, 1e-4
+
+
+@pytest.fixture(scope="module")
+def engine(model_dir, torch_gpu):
+    e = ae.Engine.from_dir(str(model_dir))
+    yield e
+    e.close()
+
+
+@pytest.fixture(scope="module")
+def ws(engine):
+    w = engine.workspace(1 << 16, 1024)
+    yield w
+    w.close()
+
+
+def check_close(gpu, ref, label=""):
+    gpu = np.atleast_2d(gpu).astype(np.float64)
+    ref = np.atleast_2d(ref).astype(np.float64)
+    cos = (gpu * ref).sum(1) / (np.linalg.norm(gpu, axis=1) * np.linalg.norm(ref, axis=1))
+    mx = np.abs(gpu - ref).max()
+    print("%s min cos %.9f max abs %.3g" % (label, cos.min(), mx), flush=True)
+    assert cos.min() >= COS_MIN and mx <= MAXABS, (cos.min(), mx)
+
+
+def test_c1_matches_golden_and_oracle(engine, ws, oracle_model):
+    ids = c1_ids()
+    e = engine.embed_tokens(ws, ids)
+    gold = np.array(json.load(open(os.path.join(GOLDEN, "oracle_golden.json")))["c1_embedding"], np.float32)
+    check_close(e, gold, "C1 vs golden")
+    check_close(e, oracle_model.forward_cls(ids), "C1 vs oracle")
+    assert abs(np.linalg.norm(e.astype(np.float64)) - 1) < 1e-5
+
+
+def test_ragged_batch_matches_oracle(engine, ws, oracle_model):
+    gold = json.load(open(os.path.join(GOLDEN, "oracle_golden.json")))["ragged_seed3_n8_16_96"]
+    seqs = ragged_batch(8, 16, 96, 3)
+    out = engine.embed_batch_tokens(ws, seqs)
+    check_close(out, np.array(gold, np.float32), "ragged8 vs golden")
+
+
+def test_edge_lengths_match_oracle(engine, ws, oracle_model):
+    rng = np.random.default_rng(5)
+    seqs = [np.array([101], np.uint16), np.array([101, 102], np.uint16)]
+    for L in (3, 63, 64, 65, 127, 129, 511, 512, 700):
+        seqs.append(np.concatenate([[101], rng.integers(1000, 30522, L - 2), [102]]).astype(np.uint16))
+    out = engine.embed_batch_tokens(ws, seqs)
+    ref = np.stack([oracle_model.forward_cls(s) for s in seqs])  # 700 truncates to 512 on both sides
+    check_close(out, ref, "edge lengths")
+
+
+def test_ragged_equals_single_bit_exact(engine, ws):
+    seqs = ragged_batch(12, 2, 200, 8)
+    batch = engine.embed_batch_tokens(ws, seqs)
+    for i in (0, 5, 11):
+        assert np.array_equal(batch[i], engine.embed_tokens(ws, seqs[i]))
+    perm = np.random.default_rng(0).permutation(len(seqs))
+    assert np.array_equal(engine.embed_batch_tokens(ws, [seqs[i] for i in perm]), batch[perm])
+
+
+def test_small_workspace_splits_batches(engine, ws):
+    small = engine.workspace(512, 4)
+    seqs = ragged_batch(19, 2, 300, 9)
+    a = engine.embed_batch_tokens(small, seqs)
+    b = engine.embed_batch_tokens(ws, seqs)
+    assert np.array_equal(a, b)
+    small.close()
+
+
+def test_packed_device_entry_point(engine, ws, torch_gpu):
+    torch = torch_gpu
+    seqs = ragged_batch(10, 5, 120, 10)
+    ref = engine.embed_batch_tokens(ws, seqs)
+    ids = torch.from_numpy(np.concatenate(seqs).astype(np.int16)).cuda()
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum([len(s) for s in seqs])]).astype(np.int32)).cuda()
+    out = torch.zeros((len(seqs), 384), dtype=torch.float32, device="cuda")
+    engine.forward_packed_device(ws, ids.data_ptr(), cu.data_ptr(), len(seqs), int(cu[-1]), out.data_ptr(),
+                                 ws.stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref)  # same order as given on the device path
+
+
+def test_text_api(engine, ws):
+    tok = ae.Tokenizer(os.path.join(GOLDEN, "vocab.txt"))
+    q = engine.embed_query(ws, "what is snowflake?")
+    assert np.array_equal(q, engine.embed_tokens(ws, tok.encode_query("what is snowflake?")))
+    docs = ["The quick brown fox.", "Snowflake's Data Cloud", "café au lait", ""]
+    batch = engine.embed_batch(ws, docs, is_query=False, num_threads=3)
+    for i, d in enumerate(docs):
+        assert np.array_equal(batch[i], engine.embed_document(ws, d))
+    assert engine.embed_batch(ws, []).shape == (0, 384)
+
+
+def test_errors(engine, ws):
+    with pytest.raises(ae.AeError) as e:
+        engine.embed_tokens(ws, np.zeros(0, np.uint16))
+    assert e.value.code == ae.AE_ERR_INVALID_ARG
+    with pytest.raises(ae.AeError) as e:
+        engine.embed_tokens(ws, np.array([101, 30522, 102], np.uint16))
+    assert e.value.code == ae.AE_ERR_INVALID_ARG
+    assert engine.size_bytes() > 33_000_000
+    assert engine.raw_size_bytes() == 33816304
+
+
+def test_kernel_timing(engine, ws):
+    ws.set_timing(True)
+    engine.embed_batch_tokens(ws, ragged_batch(4, 16, 64, 1))
+    t = ws.kernel_times()
+    ws.set_timing(False)
+    assert t["gemm_ffn_up"][1] == 11 and t["attention"][1] == 11 and t["embed_ln"][1] == 1
+    assert all(v[0] >= 0 for v in t.values())
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c4", "c5"])
+def test_full_size_configs(engine, oracle_model, cfg):
+    """BASELINE configs[2..4] at full size: size-independent properties on every
+    row (unit norm, finite) and oracle parity on a sample of rows."""
+    seqs = {"c3": lambda: ragged_batch(256, 16, 512, 3), "c4": lambda: ragged_batch(64, 512, 512, 4),
+            "c5": lambda: ragged_batch(8192, 8, 64, 5)}[cfg]()
+    T = sum(len(s) for s in seqs)
+    big = engine.workspace(T, len(seqs))
+    out = engine.embed_batch_tokens(big, seqs)
+    big.close()
+    assert np.all(np.isfinite(out))
+    assert np.abs(np.linalg.norm(out.astype(np.float64), axis=1) - 1).max() < 1e-5
+    idx = np.random.default_rng(0).choice(len(seqs), 3 if cfg != "c5" else 24, replace=False)
+    ref = np.stack([oracle_model.forward_cls(seqs[i]) for i in idx])
+    check_close(out[idx], ref, cfg + " sample")

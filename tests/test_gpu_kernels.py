@@ -1,0 +1,201 @@
+"""Kernel-level parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bar: bit-exact for every GEMM output (int32 accumulators + the f32 fma epilogue)
+and every int8 activation / scale on identical inputs; attention (f32, a
+different summation order) within the tolerance stated in its test.
+"""
+import numpy as np
+import pytest
+
+import arctic_embed_amd as ae
+import oracle as orc
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+SHAPES = [(1152, 384), (384, 384), (1536, 384), (384, 1536), (768, 384)]
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, f32).view(np.uint32)
+
+
+def linear_inputs(n, k, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = (0.05 / 127 * rng.uniform(0.5, 1.5, n)).astype(f32)
+    b = rng.normal(0, 0.02, n).astype(f32)
+    s = rng.uniform(0.5, 2.0, k).astype(f32) ** -1
+    return w, ws, b, s.astype(f32)
+
+
+@pytest.mark.parametrize("n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 37, 200])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_gemm_bit_exact(torch_gpu, n, k, m, with_res):
+    torch = torch_gpu
+    w, ws, b, s = linear_inputs(n, k, n + k + m)
+    rng = np.random.default_rng(m)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    res = rng.normal(0, 1, (m, n)).astype(f32) if with_res else None
+    lin = ae.Linear(w, ws, b, s)
+    a_d, sa_d = dev(torch, a), dev(torch, sa)
+    res_d = dev(torch, res) if with_res else None
+    out_d = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    lin.gemm(m, a_d.data_ptr(), sa_d.data_ptr(), res_d.data_ptr() if with_res else None, out_d.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.gemm(a, sa, w, ws, b, res)
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
+
+
+def test_gemm_extreme_accumulators(torch_gpu):
+    torch = torch_gpu
+    n, k, m = 128, 1536, 3
+    w = np.full((n, k), 127, np.int8)
+    w[1::2] = -127
+    a = np.full((m, k), 127, np.int8)
+    a[1] = -127
+    a[2, ::3] = -127
+    lin = ae.Linear(w, np.ones(n, f32), np.zeros(n, f32), np.ones(k, f32))
+    a_d, sa_d = dev(torch, a), dev(torch, np.ones(m, f32))
+    out_d = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    lin.gemm(m, a_d.data_ptr(), sa_d.data_ptr(), None, out_d.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.gemm(a, np.ones(m, f32), w, np.ones(n, f32), np.zeros(n, f32))
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
+    assert ref[0, 0] == f32(1536 * 127 * 127)
+
+
+@pytest.mark.parametrize("smooth", [True, False])
+@pytest.mark.parametrize("n,k", [(384, 384), (384, 1536)])
+def test_gemm_quantize_on_load_bit_exact(torch_gpu, smooth, n, k):
+    """attn_out / FFN-down GEMM: A = smooth_quantize(f32 rows) inside the GEMM prologue."""
+    torch = torch_gpu
+    m = 70
+    w, ws, b, s = linear_inputs(n, k, 7 + k)
+    rng = np.random.default_rng(k)
+    x = rng.normal(0, 1.5, (m, k)).astype(f32)
+    x[3] = 0.0  # zero row -> max_abs floor 1e-8
+    res = rng.normal(0, 1, (m, n)).astype(f32)
+    sv = s if smooth else np.ones(k, f32)
+    rowmax = np.maximum(np.abs(x * sv).max(1), f32(1e-8)).astype(f32)
+    lin = ae.Linear(w, ws, b, s)
+    x_d, rm_d, res_d = dev(torch, x), dev(torch, rowmax.view(np.uint32).astype(np.int32)), dev(torch, res)
+    s_d = dev(torch, s)
+    out_d = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    lin.gemm_quant_a(m, x_d.data_ptr(), rm_d.data_ptr(), s_d.data_ptr() if smooth else None, res_d.data_ptr(),
+                     out_d.data_ptr())
+    torch.cuda.synchronize()
+    q, sc = orc.smooth_quant_rows(x, sv)  # src/simd_math.rs:513-530
+    ref = orc.gemm(q, sc, w, ws, b, res)
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
+
+
+@pytest.mark.parametrize("m", [1, 45, 130])
+def test_gemm_gelu_epilogue_bit_exact(torch_gpu, m):
+    """FFN-up GEMM with the GELU * inv_smooth epilogue and the row absmax."""
+    torch = torch_gpu
+    n, k = 1536, 384
+    w, ws, b, s = linear_inputs(n, k, 99)
+    rng = np.random.default_rng(m + 5)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    g_smooth = rng.uniform(0.5, 2.0, n).astype(f32) ** -1
+    g_smooth = g_smooth.astype(f32)
+    lin = ae.Linear(w, ws, b, s)
+    a_d, sa_d, gs_d = dev(torch, a), dev(torch, sa), dev(torch, g_smooth)
+    rm_d = dev(torch, np.full(m, f32(1e-8)).view(np.uint32).astype(np.int32))
+    out_d = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    lin.gemm_gelu(m, a_d.data_ptr(), sa_d.data_ptr(), gs_d.data_ptr(), out_d.data_ptr(), rm_d.data_ptr())
+    torch.cuda.synchronize()
+    pre = orc.gemm(a, sa, w, ws, b)
+    g, q, sc = orc.gelu_quant_rows(pre, g_smooth)  # src/simd_math.rs:1295-1312
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(g))
+    rowmax = rm_d.cpu().numpy().astype(np.int64).astype(np.uint32).view(f32)
+    assert np.array_equal(rowmax / f32(127), sc)
+
+
+@pytest.mark.parametrize("m", [1, 31, 33, 100])
+def test_layernorm_quant_bit_exact(torch_gpu, m):
+    torch = torch_gpu
+    rng = np.random.default_rng(m)
+    x = rng.normal(0.2, 3.0, (m, 384)).astype(f32)
+    if m > 2:
+        x[1] = 0.0
+        x[2, 0], x[2, -1] = 1e8, -1e8  # order-sensitive row
+    g = (1 + 0.05 * rng.normal(size=384)).astype(f32)
+    b = (0.02 * rng.normal(size=384)).astype(f32)
+    s = (rng.uniform(0.5, 2, 384) ** -1).astype(f32)
+    x_d, g_d, b_d, s_d = dev(torch, x), dev(torch, g), dev(torch, b), dev(torch, s)
+    q_d = torch.zeros((m, 384), dtype=torch.int8, device="cuda")
+    sc_d = torch.zeros(m, dtype=torch.float32, device="cuda")
+    ae.layernorm_smooth_quantize(m, x_d.data_ptr(), g_d.data_ptr(), b_d.data_ptr(), s_d.data_ptr(), q_d.data_ptr(),
+                                 sc_d.data_ptr())
+    torch.cuda.synchronize()
+    y, q, sc = orc.ln_quant_rows(x, g, b, s)
+    assert np.array_equal(bits(x_d.cpu().numpy()), bits(y))
+    assert np.array_equal(q_d.cpu().numpy(), q)
+    assert np.array_equal(bits(sc_d.cpu().numpy()), bits(sc))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+@pytest.mark.parametrize("n", [384, 1536])
+def test_row_quantizers_bit_exact(torch_gpu, gelu, n):
+    torch = torch_gpu
+    m = 9
+    rng = np.random.default_rng(n + gelu)
+    x = rng.normal(0, 2.5, (m, n)).astype(f32)
+    x[0] = 0.0
+    x[1, :4] = [np.inf, -np.inf, np.nan, 1.0]
+    s = (rng.uniform(0.5, 2, n) ** -1).astype(f32)
+    x_d, s_d = dev(torch, x), dev(torch, s)
+    q_d = torch.zeros((m, n), dtype=torch.int8, device="cuda")
+    sc_d = torch.zeros(m, dtype=torch.float32, device="cuda")
+    fn = ae.gelu_smooth_quantize if gelu else ae.smooth_quantize
+    fn(m, n, x_d.data_ptr(), s_d.data_ptr(), q_d.data_ptr(), sc_d.data_ptr())
+    torch.cuda.synchronize()
+    if gelu:
+        gx, q, sc = orc.gelu_quant_rows(x, s)
+        assert np.array_equal(bits(x_d.cpu().numpy()), bits(gx))
+    else:
+        q, sc = orc.smooth_quant_rows(x, s)
+    assert np.array_equal(q_d.cpu().numpy(), q)
+    assert np.array_equal(bits(sc_d.cpu().numpy()), bits(sc))
+
+
+def test_gelu_bit_exact_over_float_sample(torch_gpu):
+    """GPU GELU (exact glibc-expf restatement) vs the oracle on every 61st f32 bit pattern."""
+    torch = torch_gpu
+    pat = np.arange(0, 2 ** 32, 61, dtype=np.uint64).astype(np.uint32)
+    x = pat.view(f32)
+    x_d = dev(torch, x)
+    y_d = torch.empty_like(x_d)
+    ae.gelu_map(x_d.data_ptr(), y_d.data_ptr(), x.size)
+    torch.cuda.synchronize()
+    y = y_d.cpu().numpy()
+    ref = orc.gelu(x)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(y), nan)
+    assert np.array_equal(bits(y)[~nan], bits(ref)[~nan])
+
+
+def test_attention_matches_oracle(torch_gpu):
+    """Segment-bounded attention: f32, summation order differs from the scalar
+    reference, so the bar is max |gpu - oracle| <= 2e-6 + 2e-5 * max|V|."""
+    torch = torch_gpu
+    lens = [1, 2, 17, 64, 65, 130, 512, 3]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    rng = np.random.default_rng(21)
+    qkv = rng.normal(0, 1.0, (T, 1152)).astype(f32)
+    qkv_d, cu_d = dev(torch, qkv), dev(torch, cu)
+    ctx_d = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+    ae.attention_varlen(qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, ctx_d.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.attention(qkv, cu)
+    err = np.abs(ctx_d.cpu().numpy() - ref).max()
+    assert err <= 2e-6 + 2e-5 * np.abs(qkv[:, 768:]).max(), err

@@ -1,0 +1,291 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity checker.
+
+Each check is independent of the oracle's own formula: exact integer
+arithmetic, the definition of correct rounding, closed-form known answers,
+float64 textbook formulas, and structural invariants of the reference's
+forward pass (src/model.rs).
+"""
+import hashlib
+import json
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import GOLDEN, MODEL_SHA256, c1_ids, ragged_batch
+
+f32 = np.float32
+
+
+def nearest_f32(x: Fraction):
+    """Correctly rounded (ties-to-even) float32 of an exact rational."""
+    c = f32(float(x))  # within 1 ulp of the answer
+    best = None
+    for cand in (np.nextafter(c, f32(-np.inf)), c, np.nextafter(c, f32(np.inf))):
+        d = abs(Fraction(float(cand)) - x)
+        if best is None or d < best[0] or (d == best[0] and (int(cand.view(np.uint32)) & 1) == 0):
+            best = (d, cand)
+    return best[1]
+
+
+# ---- GEMM: gemm_scalar_fused (src/gemm.rs:2000-2029) ----------------------------
+
+def test_gemm_accumulators_exact():
+    rng = np.random.default_rng(0)
+    for (m, n, k) in [(1, 16, 384), (5, 48, 384), (3, 32, 1536)]:
+        a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+        w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ref = a.astype(np.int64) @ w.astype(np.int64).T
+        assert np.array_equal(orc.gemm_acc(a, w), ref.astype(np.int32))
+
+
+def test_gemm_max_accumulator_needs_rounding():
+    # |acc| up to 1536*127^2 = 24.8M > 2^24: the f32 conversion rounds (RNE)
+    a = np.full((1, 1536), 127, np.int8)
+    w = np.full((128, 1536), 127, np.int8)
+    out = orc.gemm(a, [1.0], w, np.ones(128, f32), np.zeros(128, f32))
+    assert out[0, 0] == f32(1536 * 127 * 127)  # 24774144 is representable
+    w[0, 0] = 126  # acc = 24774017, odd and > 2^24: must round to even
+    out = orc.gemm(a, [1.0], w, np.ones(128, f32), np.zeros(128, f32))
+    assert out[0, 0] == f32(24774016.0)
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+def test_gemm_epilogue_is_single_fma(with_res):
+    rng = np.random.default_rng(1 + with_res)
+    m, n, k = 4, 32, 384
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    ws = rng.uniform(2e-4, 6e-4, n).astype(f32)
+    b = (rng.normal(0, 0.02, n)).astype(f32)
+    res = rng.normal(0, 1, (m, n)).astype(f32) if with_res else None
+    out = orc.gemm(a, sa, w, ws, b, res)
+    acc = a.astype(np.int64) @ w.astype(np.int64).T
+    for r in range(m):
+        for c in range(n):
+            prod = f32(sa[r]) * f32(ws[c])             # one f32 multiply
+            bval = b[c] + res[r, c] if with_res else b[c]  # one f32 add
+            exact = Fraction(float(f32(acc[r, c]))) * Fraction(float(prod)) + Fraction(float(bval))
+            assert out[r, c] == nearest_f32(exact), (r, c)
+
+
+# ---- quantizers (src/simd_math.rs:208-247, 513-530, 1295-1312) -----------------
+
+def test_smooth_quant_round_half_away_from_zero():
+    x = np.zeros((1, 384), f32)
+    x[0, :6] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5]
+    q, sc = orc.smooth_quant_rows(x, np.ones(384, f32))
+    assert sc[0] == f32(127.0) / f32(127.0)
+    assert list(q[0, :6]) == [127, 3, -3, 1, -1, 2]  # RNE would give 2, -2, 0, 0, 2
+
+
+def test_smooth_quant_zero_row_floor():
+    q, sc = orc.smooth_quant_rows(np.zeros((1, 384), f32), np.ones(384, f32))
+    assert sc[0] == f32(1e-8) / f32(127.0)
+    assert not q.any()
+
+
+def test_smooth_quant_uses_product_then_scale():
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, (8, 384)).astype(f32)
+    s = rng.uniform(0.5, 2.0, 384).astype(f32)
+    q, sc = orc.smooth_quant_rows(x, s)
+    ys = x * s
+    mx = np.maximum(np.abs(ys).max(axis=1), f32(1e-8))
+    assert np.array_equal(sc, mx / f32(127))
+    # |q| <= 127, the max element maps to +-127, and q is within 0.5 of y*s*127/max
+    assert np.abs(q).max() == 127
+    approx = ys * (127.0 / mx[:, None])
+    assert np.all(np.abs(q - approx) <= 0.5 + 1e-4)
+
+
+def test_layernorm_sequential_sum_known_answer():
+    # [1e8, 1 x 382, -1e8]: a left-to-right f32 sum is exactly 0 (each +1 is lost
+    # below ulp(1e8) = 8); pairwise or exact summation would give ~382.
+    x = np.ones((1, 384), f32)
+    x[0, 0], x[0, -1] = 1e8, -1e8
+    y = orc.ln_rows(x, np.ones(384, f32), np.zeros(384, f32))
+    var_sum = f32(2) * f32(1e16)          # each 1.0 is lost below ulp(1e16)
+    rstd = f32(1) / np.sqrt(var_sum / f32(384) + f32(1e-12))
+    assert y[0, 1] == f32(1) * rstd * f32(1) + f32(0)   # mean == 0 exactly
+    assert y[0, 0] == f32(1e8) * rstd
+
+
+def test_layernorm_matches_textbook_f64():
+    rng = np.random.default_rng(4)
+    x = rng.normal(0.3, 2.0, (16, 384)).astype(f32)
+    g = (1 + 0.05 * rng.normal(size=384)).astype(f32)
+    b = (0.02 * rng.normal(size=384)).astype(f32)
+    s = rng.uniform(0.5, 2.0, 384).astype(f32)
+    y, q, sc = orc.ln_quant_rows(x, g, b, s)
+    xd = x.astype(np.float64)
+    ref = (xd - xd.mean(1, keepdims=True)) / np.sqrt(xd.var(1, keepdims=True) + 1e-12) * g + b
+    assert np.abs(y - ref).max() < 2e-5
+    ys = y * s
+    assert np.array_equal(sc, np.maximum(np.abs(ys).max(1), f32(1e-8)) / f32(127))
+    assert np.all(np.abs(q - ys * (f32(127) / (sc * f32(127)))[:, None]) <= 0.5 + 1e-3)
+
+
+def test_gelu_matches_erf_gelu():
+    from math import erf, sqrt
+    xs = np.concatenate([np.linspace(-12, 12, 20001), [0.0, -0.0, 1e-30, -1e-30, 40.0, -40.0]]).astype(f32)
+    g = orc.gelu(xs)
+    ref = np.array([0.5 * float(v) * (1 + erf(float(v) / sqrt(2))) for v in xs])
+    # A&S 7.1.26 erf error <= 1.5e-7, times 0.5|x|, plus f32 rounding
+    assert np.all(np.abs(g - ref) <= 1.5e-7 * 0.5 * np.abs(xs) + 2e-7 * np.maximum(1, np.abs(ref)))
+    assert g[np.argmax(xs == 40.0)] == f32(40.0)
+    assert g[np.argmax(xs == -40.0)] == 0.0
+
+
+def test_gelu_quant_row():
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 2, (4, 1536)).astype(f32)
+    s = rng.uniform(0.5, 2, 1536).astype(f32)
+    g, q, sc = orc.gelu_quant_rows(x, s)
+    assert np.array_equal(g, orc.gelu(x) * s)
+    assert np.array_equal(sc, np.maximum(np.abs(g).max(1), f32(1e-8)) / f32(127))
+    assert np.abs(q).max() == 127
+
+
+# ---- attention pieces (src/simd_math.rs:1461-1821) --------------------------------
+
+def test_softmax_properties():
+    rng = np.random.default_rng(6)
+    s = rng.normal(0, 3, 300).astype(f32)
+    p = orc.softmax(s)
+    ref = np.exp(s.astype(np.float64) - s.max())
+    ref /= ref.sum()
+    assert abs(p.astype(np.float64).sum() - 1) < 1e-5
+    assert np.abs(p - ref).max() < 1e-6
+    # subtracting the max first makes softmax exactly invariant to a shift that is
+    # exact in f32 (scores on a 2^-10 grid shifted by 2.0)
+    s = (rng.integers(-4000, 4000, 300) * 2.0 ** -10).astype(f32)
+    assert np.array_equal(orc.softmax(s + f32(2.0)), orc.softmax(s))
+
+
+def test_attention_matches_f64():
+    rng = np.random.default_rng(7)
+    cu = np.array([0, 1, 3, 20, 84], np.int32)
+    T = cu[-1]
+    qkv = rng.normal(0, 1, (T, 1152)).astype(f32)
+    ctx = orc.attention(qkv, cu)
+    q = qkv[:, :384].astype(np.float64)
+    k = qkv[:, 384:768].astype(np.float64)
+    v = qkv[:, 768:].astype(np.float64)
+    ref = np.zeros((T, 384))
+    for b in range(len(cu) - 1):
+        a, e = cu[b], cu[b + 1]
+        for h in range(12):
+            sl = slice(h * 32, h * 32 + 32)
+            s = q[a:e, sl] @ k[a:e, sl].T / np.sqrt(32)
+            p = np.exp(s - s.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            ref[a:e, sl] = p @ v[a:e, sl]
+    assert np.abs(ctx - ref).max() < 2e-6
+    # a single-token segment returns its own V row exactly
+    assert np.array_equal(ctx[0], qkv[0, 768:])
+
+
+def test_dot32_sequential_order():
+    a = np.zeros(32, f32)
+    b = np.ones(32, f32)
+    a[0], a[1], a[31] = 1e8, 1.0, -1e8
+    assert orc.dot32(a, b) == 0.0  # the +1 is lost before -1e8 arrives
+
+
+def test_embedding_row_exact():
+    rng = np.random.default_rng(8)
+    w = rng.integers(-127, 128, 384, dtype=np.int8)
+    p = rng.integers(-127, 128, 384, dtype=np.int8)
+    t = (rng.integers(-64, 64, 384) * 2.0 ** -12).astype(f32)
+    h = orc.emb_row(w, 2.0 ** -7, p, 2.0 ** -9, t)
+    assert np.array_equal(h, (w * 2.0 ** -7 + p * 2.0 ** -9 + t.astype(np.float64)).astype(f32))
+
+
+def test_l2_normalize():
+    rng = np.random.default_rng(9)
+    v = rng.normal(0, 3, 384).astype(f32)
+    u = orc.l2(v)
+    assert abs(np.linalg.norm(u.astype(np.float64)) - 1) < 1e-6
+    assert np.abs(u - v / np.linalg.norm(v.astype(np.float64))).max() < 1e-7
+    assert not orc.l2(np.zeros(384, f32)).any()
+
+
+# ---- .ae8 format (src/quantize.rs:76-208) ------------------------------------------
+
+def test_synthetic_pack_is_deterministic(model_dir):
+    data = open(str(model_dir / "model.ae8"), "rb").read()
+    assert hashlib.sha256(data).hexdigest() == MODEL_SHA256
+
+
+def test_size_bytes_matches_layout(model_dir, oracle_model):
+    fsize = os.path.getsize(str(model_dir / "model.ae8"))
+    # headers: magic 8 + 8 embedding vectors * 8; per layer: linears * (16 + 4*8),
+    # 4 LayerNorm vectors * 8, 1 split byte; layer 11 has 6 linears
+    headers = 8 + 8 * 8 + 11 * (4 * 48 + 32 + 1) + (6 * 48 + 32 + 1)
+    assert oracle_model.size_bytes() == fsize - headers
+    assert oracle_model.size_bytes() == 33816304
+    L11 = oracle_model.layer(11)
+    assert L11.qkv.n_out == 0 and L11.qkv.is_len == 384 and L11.has_split == 1
+    assert oracle_model.layer(10).has_split == 0
+
+
+def test_loader_errors(tmp_path, model_dir):
+    data = open(str(model_dir / "model.ae8"), "rb").read()
+    assert orc.load_status(str(tmp_path / "missing.ae8")) == orc.OR_ERR_IO
+    bad = tmp_path / "bad.ae8"
+    bad.write_bytes(b"ARCTIC8\x02" + data[8:1000])
+    assert orc.load_status(str(bad)) == orc.OR_ERR_INVALID_DATA
+    for cut in (0, 5, 8, 12, 1000, len(data) // 2, len(data) - 1):
+        t = tmp_path / ("trunc%d.ae8" % cut)
+        t.write_bytes(data[:cut])
+        assert orc.load_status(str(t)) == orc.OR_ERR_EOF, cut
+    ok = tmp_path / "trailing.ae8"
+    ok.write_bytes(data + b"extra")  # trailing bytes are ignored
+    assert orc.load_status(str(ok)) == orc.OR_OK
+
+
+# ---- forward-pass invariants (src/model.rs:185-914, src/lib.rs:138-260) ------------
+
+def test_forward_unit_norm_and_golden(oracle_model):
+    e = oracle_model.forward_cls(c1_ids())
+    assert abs(np.linalg.norm(e.astype(np.float64)) - 1) < 1e-6
+    gold = json.load(open(os.path.join(GOLDEN, "oracle_golden.json")))
+    assert np.array_equal(e, np.array(gold["c1_embedding"], f32))
+
+
+def test_cls_pruning_is_exact(oracle_model):
+    for ids in ragged_batch(3, 2, 40, 11):
+        assert np.array_equal(oracle_model.forward_cls(ids), oracle_model.forward_cls_unpruned(ids))
+
+
+def test_ragged_equals_single(oracle_model):
+    seqs = ragged_batch(5, 3, 40, 12)
+    r = oracle_model.forward_ragged_cls(seqs)
+    for i, s in enumerate(seqs):
+        assert np.array_equal(r[i], oracle_model.forward_cls(s))
+
+
+def test_ragged_pack_truncates_to_512_total(oracle_model):
+    # forward_ragged_cls clips later segments to the remaining 512-token room (src/model.rs:550)
+    seqs = ragged_batch(2, 300, 300, 13)
+    r = oracle_model.forward_ragged_cls(seqs)
+    assert np.array_equal(r[1], oracle_model.forward_cls(seqs[1][:212]))
+
+
+def test_batch_policy_matches_single(oracle_model):
+    seqs = ragged_batch(9, 2, 20, 14) + ragged_batch(2, 16, 30, 15)
+    single = np.stack([oracle_model.forward_cls(s) for s in seqs])
+    for threads in (1, 3):
+        assert np.array_equal(oracle_model.embed_batch_tokens(seqs, threads), single)
+
+
+def test_truncation_and_empty(oracle_model):
+    rng = np.random.default_rng(16)
+    ids = rng.integers(1000, 30522, 600).astype(np.uint16)
+    assert np.array_equal(oracle_model.forward_cls(ids), oracle_model.forward_cls(ids[:512]))
+    with pytest.raises(ValueError):
+        oracle_model.forward_cls(np.zeros(0, np.uint16))
