@@ -107,7 +107,8 @@ def main():
     stream = torch.cuda.ExternalStream(ws.stream)
 
     def step():
-        engine.forward_packed_device(ws, ids_d.data_ptr(), cu_d.data_ptr(), B, T, out_d.data_ptr(), ws.stream)
+        engine.forward_packed_device(ws, ids_d.data_ptr(), cu_d.data_ptr(), B, T, out_d.data_ptr(), ws.stream,
+                                     max_seq_len=max(lens))
 
     for _ in range(args.warmup):
         step()
@@ -155,13 +156,13 @@ def main():
     out1 = torch.zeros((1, 384), dtype=torch.float32, device="cuda")
     s1 = torch.cuda.ExternalStream(ws1.stream)
     for _ in range(3):
-        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream)
+        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream, 128)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s1)
     n1 = 50
     for _ in range(n1):
-        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream)
+        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream, 128)
     e1.record(s1)
     torch.cuda.synchronize()
     c1_ms = e0.elapsed_time(e1) / n1

@@ -105,11 +105,12 @@ int ae_embed_batch_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* 
                           const uint32_t* offsets, size_t n, float* out);
 /* PackedModel::forward_ragged_cls (src/model.rs:521-914) with device-resident
  * inputs: ids_dev[total_tokens] u16, cu_seqlens_dev[n_seqs+1] i32 (each sequence
- * 1..512 tokens), out_dev[n_seqs*384] f32.  Asynchronous on `stream`; no host
- * copies.  Used when the caller keeps token ids in HBM. */
+ * 1..max_seq_len tokens; max_seq_len <= 512, 0 means 512), out_dev[n_seqs*384]
+ * f32.  Asynchronous on `stream`; no host copies.  Used when the caller keeps
+ * token ids in HBM. */
 int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev,
                              const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
-                             float* out_dev, void* stream);
+                             int max_seq_len, float* out_dev, void* stream);
 
 /* ---- tokenizer (host only) ---------------------------------------------- */
 /* BertTokenizer::from_vocab_file (src/tokenizer.rs:34-37). */
@@ -186,6 +187,12 @@ int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const u
  * rowmax[m] = max(rowmax[m], max_n |g|) on f32 bits (caller pre-sets rowmax). */
 int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
                        const float* g_smooth_dev, float* out_dev, uint32_t* rowmax_dev, void* stream);
+/* Embedding + the first `layers` (0..11) encoder layers over one packed batch of n
+ * sequences (given order, each 1..512 ids); copies back hidden [T,384] f32,
+ * act_q [T,384] int8 and act_scale [T] (T = offsets[n]), the state that
+ * src/model.rs:593-768 leaves after those layers. */
+int ae_debug_forward_prefix(const ae_engine* e, ae_workspace* ws, const uint16_t* ids, const uint32_t* offsets,
+                            size_t n, int layers, float* hidden, int8_t* act_q, float* act_scale);
 /* Device GELU (the reference's scalar_gelu, src/simd_math.rs:15-23) over n floats. */
 int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream);
 

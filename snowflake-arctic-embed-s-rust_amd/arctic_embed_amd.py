@@ -24,6 +24,16 @@ LIB_PATH = os.path.join(_HERE, "libarctic_embed_amd.so")
 if not os.path.exists(LIB_PATH):
     raise ImportError(
         "libarctic_embed_amd.so is not built (run __graft_entry__.build() or make -C %s)" % _HERE)
+
+# One process must hold one HIP runtime.  PyTorch-ROCm ships its own
+# libamdhip64 (SONAME libamdhip64.so.7) and asks for it as "libamdhip64.so";
+# this library asks for "libamdhip64.so.7".  Loading torch first lets our
+# dependency resolve to torch's copy by SONAME; loading ours first would make
+# torch map a second runtime, and the two then fight over the device.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
 _lib = ctypes.CDLL(LIB_PATH)
 
 _c = ctypes
@@ -46,7 +56,7 @@ _SIGS = {
     "ae_embed_document": (_i32, [_vp, _vp, _c.c_char_p, _vp]),
     "ae_embed_batch": (_i32, [_vp, _vp, _c.POINTER(_c.c_char_p), _sz, _i32, _i32, _vp]),
     "ae_embed_batch_tokens": (_i32, [_vp, _vp, _vp, _vp, _sz, _vp]),
-    "ae_forward_packed_device": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "ae_forward_packed_device": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "ae_cosine_similarity": (_c.c_float, [_vp, _vp]),
     "ae_linear_create": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _c.POINTER(_vp)]),
     "ae_linear_destroy": (None, [_vp]),
@@ -62,6 +72,7 @@ _SIGS = {
     "ae_tokenizer_vocab_size": (_sz, [_vp]),
     "ae_debug_gelu_map": (_i32, [_vp, _vp, _sz, _vp]),
     "ae_workspace_set_timing": (_i32, [_vp, _i32]),
+    "ae_debug_forward_prefix": (_i32, [_vp, _vp, _vp, _vp, _sz, _i32, _vp, _vp, _vp]),
     "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
     "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_gemm_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -237,9 +248,22 @@ class Engine:
                                    out.ctypes.data))
         return out
 
-    def forward_packed_device(self, ws, ids_ptr, cu_ptr, n_seqs, total_tokens, out_ptr, stream=None):
+    def forward_prefix(self, ws, seqs, layers):
+        """Embedding + `layers` encoder layers; returns (hidden, act_q, act_scale) over packed rows."""
+        ids, offsets = _pack_ids(list(seqs))
+        T = int(offsets[-1])
+        hidden = np.zeros((T, HIDDEN), np.float32)
+        act_q = np.zeros((T, HIDDEN), np.int8)
+        scale = np.zeros(T, np.float32)
+        _check(_lib.ae_debug_forward_prefix(self._h, ws.handle, ids.ctypes.data, offsets.ctypes.data, len(offsets) - 1,
+                                            int(layers), hidden.ctypes.data, act_q.ctypes.data, scale.ctypes.data))
+        return hidden, act_q, scale
+
+    def forward_packed_device(self, ws, ids_ptr, cu_ptr, n_seqs, total_tokens, out_ptr, stream=None,
+                              max_seq_len=0):
+        """forward_ragged_cls over a packed batch already in HBM (max_seq_len 0 = 512)."""
         _check(_lib.ae_forward_packed_device(self._h, ws.handle, ids_ptr, cu_ptr, int(n_seqs),
-                                             int(total_tokens), out_ptr, stream))
+                                             int(total_tokens), int(max_seq_len), out_ptr, stream))
 
 
 class Workspace:

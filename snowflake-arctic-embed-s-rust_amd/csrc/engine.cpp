@@ -267,8 +267,12 @@ struct KernelTimer {
 
 // one forward pass over a token-packed batch already resident on the device
 // (PackedModel::forward_ragged_cls, src/model.rs:521-914, without its 64-sequence /
-// 512-token limits).  ids/cu may be the workspace's or the caller's buffers.
-int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int T, float* out, hipStream_t st) {
+// 512-token limits).  ids/cu may be the workspace's or the caller's buffers;
+// max_len bounds every sequence length (it sizes the attention score rows).
+// stop_layers >= 0 stops after the embedding and that many encoder layers
+// (a test hook that leaves hidden / act_q / act_scale in the workspace).
+int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int T, int max_len, float* out,
+                hipStream_t st, int stop_layers = -1) {
   const ae_engine* E = ws->e;
   using namespace aek;
   if (ws->timing && ws->ev_used + 2 * 80 > ws->ev_pool.size()) {
@@ -331,8 +335,10 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.rowmax_init = ws->rowmax_ctx;
     launch_ln_quant(p, kLnSrcEmb, st);
   }
-  const int max_tiles = T / 64 + B + 1;
+  const int max_tiles = T / 32 + B + 1;  // >= sum_b ceil(L_b / 32)
+  const int s_pitch = attention_pitch(max_len);
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
+    if (stop_layers >= 0 && l >= stop_layers) break;
     const DevLayer& D = E->layers[l];
     {
       KernelTimer kt(ws, st, AE_KERNEL_GEMM_QKV);
@@ -340,7 +346,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
-      AttnArgs a{ws->qkv, cu, B, ws->tile_start, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx};
+      AttnArgs a{ws->qkv, cu, B, ws->tile_start, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
       launch_attention(a, max_tiles, st);
     }
     {
@@ -367,6 +373,10 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       ln(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q, ws->act_scale,
          ws->rowmax_ctx, T);
     }
+  }
+  if (stop_layers >= 0) {
+    hipError_t err = hipGetLastError();
+    return err == hipSuccess ? AE_OK : fail(AE_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(err));
   }
   // layer 11: [CLS] pruning (src/model.rs:770-913)
   KernelTimer kt(ws, st, AE_KERNEL_LAYER11_TAIL);
@@ -432,7 +442,8 @@ int run_sequences(const ae_engine* e, ae_workspace* ws, const std::vector<const 
     }
     HIP_TRY(hipMemcpyAsync(ws->ids, ws->h_ids, size_t(T) * sizeof(uint16_t), hipMemcpyHostToDevice, ws->stream));
     HIP_TRY(hipMemcpyAsync(ws->cu, ws->h_cu, size_t(B + 1) * sizeof(int), hipMemcpyHostToDevice, ws->stream));
-    if (int rc = run_forward(ws, ws->ids, ws->cu, B, T, ws->out_c, ws->stream)) return rc;
+    const int max_len = lens[order[i + B - 1]];  // length-sorted: the last is the longest
+    if (int rc = run_forward(ws, ws->ids, ws->cu, B, T, max_len, ws->out_c, ws->stream)) return rc;
     HIP_TRY(hipMemcpyAsync(ws->h_out, ws->out_c, size_t(B) * ae::kHidden * sizeof(float), hipMemcpyDeviceToHost,
                            ws->stream));
     HIP_TRY(hipStreamSynchronize(ws->stream));
@@ -606,14 +617,16 @@ int ae_embed_batch(const ae_engine* e, ae_workspace* ws, const char* const* text
 }
 
 int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev, const int32_t* cu_seqlens_dev,
-                             int n_seqs, int total_tokens, float* out_dev, void* stream) {
+                             int n_seqs, int total_tokens, int max_seq_len, float* out_dev, void* stream) {
   if (!e || !ws || ws->e != e) return fail(AE_ERR_INVALID_ARG, "engine/workspace mismatch");
-  if (n_seqs <= 0 || total_tokens < n_seqs || !ids_dev || !cu_seqlens_dev || !out_dev)
+  if (n_seqs <= 0 || total_tokens < n_seqs || !ids_dev || !cu_seqlens_dev || !out_dev || max_seq_len < 0 ||
+      max_seq_len > ae::kMaxPos)
     return fail(AE_ERR_INVALID_ARG, "bad packed batch");
   if (n_seqs > ws->max_seqs || total_tokens > ws->max_tokens)
     return fail(AE_ERR_CAPACITY, "packed batch exceeds workspace capacity");
   hipStream_t st = stream ? as_stream(stream) : ws->stream;
-  return run_forward(ws, ids_dev, cu_seqlens_dev, n_seqs, total_tokens, out_dev, st);
+  return run_forward(ws, ids_dev, cu_seqlens_dev, n_seqs, total_tokens, max_seq_len ? max_seq_len : ae::kMaxPos,
+                     out_dev, st);
 }
 
 float ae_cosine_similarity(const float* a, const float* b) {  // src/lib.rs:265-271
@@ -702,8 +715,9 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   if (n_seqs == 0) return AE_OK;
   int* tile_start = nullptr;
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&tile_start), size_t(n_seqs + 1) * sizeof(int)));
-  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, tile_start, ctx_dev, nullptr, nullptr};
-  aek::launch_attention(a, total_tokens / 64 + n_seqs + 1, as_stream(stream));
+  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, tile_start, ctx_dev, nullptr, nullptr,
+                  aek::attention_pitch(ae::kMaxPos)};
+  aek::launch_attention(a, total_tokens / 32 + n_seqs + 1, as_stream(stream));
   hipError_t err = hipStreamSynchronize(as_stream(stream));
   (void)hipFree(tile_start);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));
@@ -811,6 +825,31 @@ int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const flo
   p.g_rowmax = rowmax_dev;
   aek::launch_gemm(p, aek::kAI8, aek::kEpiGelu, as_stream(stream));
   HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+// test hook: embedding + the first `layers` encoder layers over one packed batch
+// (in the given order); copies hidden [T,384], act_q [T,384], act_scale [T] back
+int ae_debug_forward_prefix(const ae_engine* e, ae_workspace* ws, const uint16_t* ids, const uint32_t* offsets,
+                            size_t n, int layers, float* hidden, int8_t* act_q, float* act_scale) {
+  if (!e || !ws || n == 0 || layers < 0 || layers > ae::kLayers - 1) return fail(AE_ERR_INVALID_ARG, "bad args");
+  const int T = int(offsets[n]);
+  if (int(n) > ws->max_seqs || T > ws->max_tokens) return fail(AE_ERR_CAPACITY, "too large");
+  int max_len = 0;
+  for (size_t i = 0; i <= n; i++) ws->h_cu[i] = int(offsets[i]);
+  for (size_t i = 0; i < n; i++) {
+    const int len = int(offsets[i + 1] - offsets[i]);
+    if (len < 1 || len > ae::kMaxPos) return fail(AE_ERR_INVALID_ARG, "sequence lengths must be 1..512");
+    max_len = std::max(max_len, len);
+  }
+  std::memcpy(ws->h_ids, ids, size_t(T) * sizeof(uint16_t));
+  HIP_TRY(hipMemcpyAsync(ws->ids, ws->h_ids, size_t(T) * sizeof(uint16_t), hipMemcpyHostToDevice, ws->stream));
+  HIP_TRY(hipMemcpyAsync(ws->cu, ws->h_cu, (n + 1) * sizeof(int), hipMemcpyHostToDevice, ws->stream));
+  if (int rc = run_forward(ws, ws->ids, ws->cu, int(n), T, max_len, nullptr, ws->stream, layers)) return rc;
+  HIP_TRY(hipMemcpyAsync(hidden, ws->hidden, size_t(T) * 384 * 4, hipMemcpyDeviceToHost, ws->stream));
+  HIP_TRY(hipMemcpyAsync(act_q, ws->act_q, size_t(T) * 384, hipMemcpyDeviceToHost, ws->stream));
+  HIP_TRY(hipMemcpyAsync(act_scale, ws->act_scale, size_t(T) * 4, hipMemcpyDeviceToHost, ws->stream));
+  HIP_TRY(hipStreamSynchronize(ws->stream));
   return AE_OK;
 }
 

@@ -2,10 +2,10 @@
 //
 // Build flags that carry semantics: -ffp-contract=off (no a*b+c fusion: the
 // reference is Rust, which never contracts), correctly rounded f32 divide and
-// sqrt (HIP's default), no fast-math.  Every kernel whose output is int8 or a
-// GEMM f32 result evaluates exactly the reference's scalar expression order, so
-// those outputs are bit-identical to the reference's scalar backend on the same
-// inputs.  Attention is f32 with a different summation order (tolerance-level).
+// sqrt (HIP's default), no fast-math.  Every kernel evaluates exactly the
+// reference's scalar expression order (sequential sums, separately rounded
+// products, glibc's expf), so its outputs are bit-identical to the reference's
+// scalar backend on the same inputs, and so is the whole forward pass.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -425,20 +425,34 @@ void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, fl
 }
 
 // ---------------------------------------------------------------------------
-// Varlen attention, head_dim 32.  tile_start[b] = sum_{b'<b} ceil(L_b'/64) is
-// built on the device from cu_seqlens; WG (tile, head) owns 64 queries of one
-// sequence; 4 lanes per query (8 dims each); keys/values stream through LDS in
-// chunks of 64 with an online softmax.  Also folds the SmoothQuant row absmax
-// of the attention output (|ctx_j * inv_smooth_j|) into `rowmax` (atomicMax on
-// the non-negative float bits), which the attn_out GEMM prologue consumes.
+// Varlen attention, head_dim 32, bit-exact with the reference's scalar path
+// (src/model.rs:663-694 with compute_scores_head32 / softmax_inplace /
+// weighted_sum_head32 scalar branches, src/simd_math.rs:1461-1821):
+//   s_t  = (sum_{i=0..31, in order} q_i*k_t,i) * (1/sqrt(32))
+//   e_t  = expf(s_t - max_t s_t)            (glibc expf, restated above)
+//   sum  = sum_{t in order} e_t ; inv = 1/sum ; p_t = e_t * inv
+//   ctx_d = sum_{t in order} p_t * v_t,d
+// every sum left to right with separately rounded products.
+//
+// WG (tile, head) owns kAttnQ queries of one sequence.  Scores for all keys of
+// the sequence stay in LDS (row pitch = padded max length); the score, exp and
+// PV phases use all 256 lanes, only the in-order softmax denominator is one
+// lane per query.  tile_start[b] = sum_{b'<b} ceil(L_b'/kAttnQ) is built on the
+// device from cu_seqlens.  Also folds the SmoothQuant row absmax of the output
+// (|ctx_j * inv_smooth_j|) into `rowmax` (atomicMax on non-negative f32 bits),
+// which the attn_out GEMM prologue consumes.
 // ---------------------------------------------------------------------------
+constexpr int kAttnQ = 32;     // queries per workgroup
+constexpr int kKeyChunk = 64;  // keys per K/V staging chunk
+constexpr int kKPitch = 36;    // K chunk row pitch (floats): conflict-free 16-byte reads
+
 __global__ __launch_bounds__(256) void tile_starts_kernel(const int* cu, int B, int* tile_start) {
   __shared__ int part[256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
   int s = 0;
-  for (int b = b0; b < b1; b++) s += (cu[b + 1] - cu[b] + 63) >> 6;
+  for (int b = b0; b < b1; b++) s += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
   part[tid] = s;
   __syncthreads();
   if (tid == 0) {
@@ -453,15 +467,17 @@ __global__ __launch_bounds__(256) void tile_starts_kernel(const int* cu, int B, 
   int acc = part[tid];
   for (int b = b0; b < b1; b++) {
     tile_start[b] = acc;
-    acc += (cu[b + 1] - cu[b] + 63) >> 6;
+    acc += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
   }
   if (b1 == B && b0 < b1) tile_start[B] = acc;
   if (B == 0 && tid == 0) tile_start[0] = 0;
 }
 
+// dynamic LDS: S[kAttnQ][s_pitch] scores/probabilities, then K/V chunk, Q tile
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) float sK[64 * 32];
-  __shared__ __attribute__((aligned(16))) float sV[64 * 32];
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ uint64_t sTab[32];
+  __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
   const int tile = blockIdx.x, h = blockIdx.y;
   if (tile >= p.tile_start[p.B]) return;
   int lo = 0, hi = p.B - 1;
@@ -470,90 +486,148 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
     if (p.tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
   }
   const int b = lo;
-  const int s0 = p.cu[b], L = p.cu[b + 1] - s0;
-  const int q0 = (tile - p.tile_start[b]) * 64;
-  const int tid = threadIdx.x, qi = tid >> 2, sub = tid & 3;
-  const int qrow = q0 + qi;
-  const bool qvalid = qrow < L;
-  const int qr = min(qrow, L - 1);
-  float q[8];
-  {
-    const float4* qs = reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + qr) * HQKV + h * 32 + sub * 8);
-    float4 a = qs[0], c = qs[1];
-    q[0] = a.x; q[1] = a.y; q[2] = a.z; q[3] = a.w; q[4] = c.x; q[5] = c.y; q[6] = c.z; q[7] = c.w;
+  const int s0 = p.cu[b];
+  const int L = min(p.cu[b + 1] - s0, p.s_pitch - 4);  // the host sizes s_pitch >= L + 4
+  const int q0 = (tile - p.tile_start[b]) * kAttnQ;
+  const int nq = min(kAttnQ, L - q0);
+  const int pitch = p.s_pitch;
+  float* S = smem;                                   // [kAttnQ][pitch]
+  float* KV = smem + kAttnQ * pitch;                 // [kKeyChunk][kKPitch]
+  float* Qs = KV + kKeyChunk * kKPitch;              // [kAttnQ][32]
+  const int tid = threadIdx.x;
+  load_exp_tab(sTab);
+  {  // Q tile (rows past the segment are clamped; their results are never stored)
+    const int r = tid >> 3, c4 = tid & 7;
+    const int qr = min(q0 + r, L - 1);
+    *reinterpret_cast<float4*>(&Qs[r * 32 + c4 * 4]) =
+        *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + qr) * HQKV + h * 32 + c4 * 4);
   }
-  float m = -INFINITY, l = 0.0f, o[8];
-#pragma unroll
-  for (int d = 0; d < 8; d++) o[d] = 0.0f;
 
-  for (int k0 = 0; k0 < L; k0 += 64) {
+  // phase 1: scores. thread -> key (tid % 64) x 8 queries (group tid / 64)
+  const int kk = tid & 63, qg = tid >> 6;
+  for (int k0 = 0; k0 < L; k0 += kKeyChunk) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int idx = tid + i * 256, key = idx >> 3, c4 = idx & 7;
-      const int kr = k0 + key;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (kr < L) {
-        const float* base = p.qkv + (size_t)(s0 + kr) * HQKV + h * 32 + c4 * 4;
-        kv = *reinterpret_cast<const float4*>(base + H);
-        vv = *reinterpret_cast<const float4*>(base + 2 * H);
-      }
-      *reinterpret_cast<float4*>(&sK[key * 32 + c4 * 4]) = kv;
-      *reinterpret_cast<float4*>(&sV[key * 32 + c4 * 4]) = vv;
+      const int kr = min(k0 + key, L - 1);
+      *reinterpret_cast<float4*>(&KV[key * kKPitch + c4 * 4]) =
+          *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + kr) * HQKV + H + h * 32 + c4 * 4);
     }
     __syncthreads();
-    const int nk = min(64, L - k0);
-    float s[64];
-    float cmax = -INFINITY;
+    float k[32];
 #pragma unroll
-    for (int j = 0; j < 64; j++) {
-      const float4 ka = *reinterpret_cast<const float4*>(&sK[j * 32 + sub * 8]);
-      const float4 kb = *reinterpret_cast<const float4*>(&sK[j * 32 + sub * 8 + 4]);
-      float d = q[0] * ka.x + q[1] * ka.y + q[2] * ka.z + q[3] * ka.w + q[4] * kb.x + q[5] * kb.y + q[6] * kb.z +
-                q[7] * kb.w;
-      d += __shfl_xor(d, 1, 64);
-      d += __shfl_xor(d, 2, 64);
-      s[j] = j < nk ? d * kInvSqrtD : -INFINITY;
-      cmax = fmaxf(cmax, s[j]);
+    for (int c = 0; c < 32; c += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&KV[kk * kKPitch + c]);
+      k[c] = v.x; k[c + 1] = v.y; k[c + 2] = v.z; k[c + 3] = v.w;
     }
-    const float mnew = fmaxf(m, cmax);
-    const float corr = __expf(m - mnew);
-    l *= corr;
+    const bool kvalid = k0 + kk < L;
+#pragma unroll 2
+    for (int j = 0; j < 8; j++) {
+      const int q = qg * 8 + j;
+      const float* qr = &Qs[q * 32];
+      float sum = 0.0f;  // dot32_f32 scalar branch: sequential, separately rounded products
 #pragma unroll
-    for (int d = 0; d < 8; d++) o[d] *= corr;
-#pragma unroll
-    for (int j = 0; j < 64; j++) {
-      const float pj = __expf(s[j] - mnew);
-      l += pj;
-      const float4 va = *reinterpret_cast<const float4*>(&sV[j * 32 + sub * 8]);
-      const float4 vb = *reinterpret_cast<const float4*>(&sV[j * 32 + sub * 8 + 4]);
-      o[0] += pj * va.x; o[1] += pj * va.y; o[2] += pj * va.z; o[3] += pj * va.w;
-      o[4] += pj * vb.x; o[5] += pj * vb.y; o[6] += pj * vb.z; o[7] += pj * vb.w;
+      for (int c = 0; c < 32; c += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(qr + c);
+        sum += v.x * k[c];
+        sum += v.y * k[c + 1];
+        sum += v.z * k[c + 2];
+        sum += v.w * k[c + 3];
+      }
+      if (kvalid) S[q * pitch + k0 + kk] = sum * kInvSqrtD;
     }
-    m = mnew;
   }
-  const float inv_l = 1.0f / l;
-  float amax = 0.0f;
+  __syncthreads();
+
+  // phase 2: row max (order-free), 8 lanes per query
+  const int rq = tid >> 3, rsub = tid & 7;
+  {
+    float m = -INFINITY;
+    for (int t = rsub; t < L; t += 8) m = nanless_max(m, S[rq * pitch + t]);
 #pragma unroll
-  for (int d = 0; d < 8; d++) {
-    o[d] = o[d] * inv_l;
-    if (p.smooth) amax = nanless_max(amax, fabsf(o[d] * p.smooth[h * 32 + sub * 8 + d]));
+    for (int off = 1; off < 8; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
+    if (rsub == 0) s_max[rq] = m;
   }
-  if (qvalid) {
-    float4* dst = reinterpret_cast<float4*>(p.ctx + (size_t)(s0 + qrow) * H + h * 32 + sub * 8);
-    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+  __syncthreads();
+  // phase 3: e_t = expf(s_t - max)
+  {
+    const float m = s_max[rq];
+    for (int t = rsub; t < L; t += 8) S[rq * pitch + t] = expf_libm(S[rq * pitch + t] - m, sTab);
   }
-  if (p.rowmax) {
-    amax = nanless_max(amax, __shfl_xor(amax, 1, 64));
-    amax = nanless_max(amax, __shfl_xor(amax, 2, 64));
-    if (qvalid && sub == 0) atomicMax(&p.rowmax[s0 + qrow], __float_as_uint(amax));
+  __syncthreads();
+  // phase 4: in-order denominator, one lane per query
+  if (tid < kAttnQ) {
+    const float* e = &S[tid * pitch];
+    float sum = 0.0f;
+    int t = 0;
+    for (; t + 4 <= L; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(e + t);
+      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    }
+    for (; t < L; t++) sum += e[t];
+    s_inv[tid] = 1.0f / sum;
+  }
+  __syncthreads();
+  // phase 5: p_t = e_t * inv
+  {
+    const float inv = s_inv[rq];
+    for (int t = rsub; t < L; t += 8) S[rq * pitch + t] = S[rq * pitch + t] * inv;
+  }
+
+  // phase 6: ctx_d = sum_t p_t * v_t,d in order. thread -> d (tid % 32) x 4 queries
+  const int d = tid & 31, pg = tid >> 5;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < L; k0 += kKeyChunk) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int idx = tid + i * 256, key = idx >> 3, c4 = idx & 7;
+      const int kr = min(k0 + key, L - 1);
+      *reinterpret_cast<float4*>(&KV[key * kKPitch + c4 * 4]) =
+          *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + kr) * HQKV + 2 * H + h * 32 + c4 * 4);
+    }
+    __syncthreads();
+    const int nk = min(kKeyChunk, L - k0);
+    for (int t = 0; t < nk; t++) {
+      const float v = KV[t * kKPitch + d];
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[j] = acc[j] + S[(pg * 4 + j) * pitch + k0 + t] * v;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int q = pg * 4 + j;
+    const float o = acc[j];
+    if (q < nq) p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = o;
+    if (p.rowmax) {
+      float a = q < nq ? fabsf(o * p.smooth[h * 32 + d]) : 0.0f;
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
+      if (q < nq && d == 0) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
+    }
   }
 }
 
+size_t attention_lds_bytes(int s_pitch) {
+  return sizeof(float) * ((size_t)kAttnQ * s_pitch + kKeyChunk * kKPitch + kAttnQ * 32);
+}
+
+int attention_pitch(int max_len) {
+  const int L = max(1, min(max_len, 512));
+  return ((L + 3) / 4) * 4 + 4;
+}
+
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
+  static bool lds_raised = false;  // once per process: allow > 64 KiB of dynamic LDS
+  if (!lds_raised) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_lds_bytes(attention_pitch(512)));
+    lds_raised = true;
+  }
   hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.tile_start);
-  if (max_tiles > 0) hipLaunchKernelGGL(attention_kernel, dim3(max_tiles, 12), dim3(256), 0, st, p);
+  if (max_tiles > 0)
+    hipLaunchKernelGGL(attention_kernel, dim3(max_tiles, 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -573,67 +647,58 @@ __global__ __launch_bounds__(128) void gather_cls_kernel(ClsArgs p) {
   }
 }
 
-// one wave per (sequence, head): the [CLS] query attends to its segment
+// one wave per (sequence, head): the [CLS] query attends to its segment with the
+// same exact scalar order as attention_kernel (src/model.rs:814-843)
 __global__ __launch_bounds__(64) void cls_attention_kernel(ClsArgs p) {
+  __shared__ uint64_t sTab[32];
+  __shared__ __attribute__((aligned(16))) float S[512];
+  __shared__ float s_inv;
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const int s0 = p.cu[b], L = p.cu[b + 1] - s0;
+  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, 512);
+  load_exp_tab(sTab);
   float q[32];
 #pragma unroll
   for (int d = 0; d < 32; d += 4) {
     const float4 v = *reinterpret_cast<const float4*>(p.q_c + (size_t)b * H + h * 32 + d);
     q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
   }
-  float sc[8];
   float m = -INFINITY;
+  for (int j = lane; j < L; j += 64) {
+    const float* kr = p.kv + (size_t)(s0 + j) * 2 * H + h * 32;
+    float sum = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int j = lane + 64 * i;
-    sc[i] = -INFINITY;
-    if (j < L) {
-      const float* kr = p.kv + (size_t)(s0 + j) * 2 * H + h * 32;
-      float d = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 32; e += 4) {
-        const float4 k = *reinterpret_cast<const float4*>(kr + e);
-        d += q[e] * k.x + q[e + 1] * k.y + q[e + 2] * k.z + q[e + 3] * k.w;
-      }
-      sc[i] = d * kInvSqrtD;
-      m = fmaxf(m, sc[i]);
+    for (int e = 0; e < 32; e += 4) {
+      const float4 k = *reinterpret_cast<const float4*>(kr + e);
+      sum += q[e] * k.x;
+      sum += q[e + 1] * k.y;
+      sum += q[e + 2] * k.z;
+      sum += q[e + 3] * k.w;
     }
+    const float sc = sum * kInvSqrtD;
+    S[j] = sc;
+    m = nanless_max(m, sc);
   }
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  float o[32];
-#pragma unroll
-  for (int d = 0; d < 32; d++) o[d] = 0.0f;
-  float l = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int j = lane + 64 * i;
-    if (j < L) {
-      const float pj = __expf(sc[i] - m);
-      l += pj;
-      const float* vr = p.kv + (size_t)(s0 + j) * 2 * H + H + h * 32;
-#pragma unroll
-      for (int e = 0; e < 32; e += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(vr + e);
-        o[e] += pj * v.x; o[e + 1] += pj * v.y; o[e + 2] += pj * v.z; o[e + 3] += pj * v.w;
-      }
-    }
+  for (int off = 1; off < 64; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
+  __syncthreads();  // also publishes sTab
+  for (int j = lane; j < L; j += 64) S[j] = expf_libm(S[j] - m, sTab);
+  __syncthreads();
+  if (lane == 0) {
+    float sum = 0.0f;
+    for (int j = 0; j < L; j++) sum += S[j];
+    s_inv = 1.0f / sum;
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    l += __shfl_xor(l, off, 64);
-#pragma unroll
-    for (int d = 0; d < 32; d++) o[d] += __shfl_xor(o[d], off, 64);
+  __syncthreads();
+  const float inv = s_inv;
+  for (int j = lane; j < L; j += 64) S[j] = S[j] * inv;
+  __syncthreads();
+  float o = 0.0f;
+  if (lane < 32) {
+    const float* vr = p.kv + (size_t)s0 * 2 * H + H + h * 32 + lane;
+    for (int t = 0; t < L; t++) o = o + S[t] * vr[(size_t)t * 2 * H];
+    p.ctx_c[(size_t)b * H + h * 32 + lane] = o;
   }
-  const float inv_l = 1.0f / l;
-  float mine = 0.0f;
-#pragma unroll
-  for (int d = 0; d < 32; d++)
-    if (lane == d) mine = o[d] * inv_l;
-  if (lane < 32) p.ctx_c[(size_t)b * H + h * 32 + lane] = mine;
-  float a = lane < 32 ? fabsf(mine * p.smooth[h * 32 + lane]) : 0.0f;
+  float a = lane < 32 ? fabsf(o * p.smooth[h * 32 + lane]) : 0.0f;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
   if (lane == 0) atomicMax(&p.rowmax_ctx_c[b], __float_as_uint(a));

@@ -68,7 +68,11 @@ struct AttnArgs {
   float* ctx;              // [T,384]
   const float* smooth;     // attn_out inv_smooth [384] or null
   uint32_t* rowmax;        // [T] or null
+  int s_pitch;             // score row pitch: attention_pitch(max sequence length)
 };
+int attention_pitch(int max_len);
+size_t attention_lds_bytes(int s_pitch);
+// tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32)
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st);
 
 struct ClsArgs {
