@@ -64,6 +64,38 @@ def kernel_work(kind, T, B, lens):
     return None
 
 
+def gemm_microbench(ae, torch, iters):
+    """standalone W8A8 GEMM, f32 output + bias, through the C ABI."""
+    rng = np.random.default_rng(2)
+    rows = []
+    for (k, n) in [(384, 1152), (384, 384), (384, 1536), (1536, 384)]:
+        w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        ws_ = rng.uniform(0.0002, 0.0006, n).astype(np.float32)
+        bias = rng.normal(0, 0.02, n).astype(np.float32)
+        lin = ae.Linear(w, ws_, bias, np.ones(k, np.float32))
+        for m in (128, 4096, 32768):
+            a = torch.from_numpy(rng.integers(-127, 128, (m, k), dtype=np.int8)).cuda()
+            sa = torch.from_numpy(rng.uniform(0.01, 0.1, m).astype(np.float32)).cuda()
+            out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            for _ in range(3):
+                lin.gemm(m, a.data_ptr(), sa.data_ptr(), None, out.data_ptr())
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                lin.gemm(m, a.data_ptr(), sa.data_ptr(), None, out.data_ptr())
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / iters
+            ops = 2.0 * m * n * k
+            byts = m * k + n * k + 4 * m + 8 * n + 4 * m * n
+            rows.append({"M": m, "K": k, "N": n, "us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
+                         "mfma_frac": round(ops / us / 1e6 / PEAK_INT8_TOPS, 4),
+                         "GBs": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / PEAK_HBM_GBS, 4)})
+        lin.close()
+    return rows
+
+
 def load_cpu_oracle():
     """The oracle (scalar restatement of the reference), used only by the cpu_baseline leg."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -79,6 +111,8 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-sample", type=int, default=32, help="sequences of the workload timed on the CPU")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-c1", action="store_true", help="skip the 128-token latency measurement")
+    ap.add_argument("--gemm", action="store_true", help="run only the configs[1] GEMM microbench")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on exactly one GPU (the forward pass is data-parallel over sequences "
@@ -87,6 +121,11 @@ def main():
 
     import torch
     import arctic_embed_amd as ae
+
+    if args.gemm:
+        rows = gemm_microbench(ae, torch, max(args.steps, 10))
+        print(json.dumps({"gemm_microbench": rows}), flush=True)
+        return
 
     tmp = tempfile.mkdtemp(prefix="ae_bench_")
     try:
@@ -149,24 +188,28 @@ def main():
         ffn[k] = round(a / s / 1e12 / p, 4)
 
     # ms/seq @ 128 tokens (BASELINE metric, part 3): single-sequence latency, device-resident input
-    c1 = make_batch(1, 128, 128, 1)[0]
-    ws1 = engine.workspace(512, 1)
-    ids1 = torch.from_numpy(c1.view(np.int16)).cuda()
-    cu1 = torch.tensor([0, 128], dtype=torch.int32, device="cuda")
-    out1 = torch.zeros((1, 384), dtype=torch.float32, device="cuda")
-    s1 = torch.cuda.ExternalStream(ws1.stream)
-    for _ in range(3):
-        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream, 128)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(s1)
-    n1 = 50
-    for _ in range(n1):
-        engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream, 128)
-    e1.record(s1)
-    torch.cuda.synchronize()
-    c1_ms = e0.elapsed_time(e1) / n1
-    ws1.close()
+    c1_ms = None
+    if not args.no_c1:
+        c1 = make_batch(1, 128, 128, 1)[0]
+        ws1 = engine.workspace(512, 1)
+        ids1 = torch.from_numpy(c1.view(np.int16)).cuda()
+        cu1 = torch.tensor([0, 128], dtype=torch.int32, device="cuda")
+        out1 = torch.zeros((1, 384), dtype=torch.float32, device="cuda")
+        s1 = torch.cuda.ExternalStream(ws1.stream)
+        for _ in range(3):
+            engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream,
+                                         128)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s1)
+        n1 = 50
+        for _ in range(n1):
+            engine.forward_packed_device(ws1, ids1.data_ptr(), cu1.data_ptr(), 1, 128, out1.data_ptr(), ws1.stream,
+                                         128)
+        e1.record(s1)
+        torch.cuda.synchronize()
+        c1_ms = round(e0.elapsed_time(e1) / n1, 4)
+        ws1.close()
 
     cpu = None
     if not args.no_cpu:
@@ -198,7 +241,7 @@ def main():
         "config": {"workload": workload, "n_seqs": B, "tokens": T, "model": "arctic-embed-s synthetic seed 0xAE85EED"},
         "tokens_per_s": round(T * args.steps / (gpu_ms / 1e3), 1),
         "wall_s": round(wall, 4), "outputs_unit_norm": norms_ok,
-        "ffn_int8_mfma_frac": ffn, "ms_per_seq_128": round(c1_ms, 4),
+        "ffn_int8_mfma_frac": ffn, "ms_per_seq_128": c1_ms,
         "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
         "roofline": roofline, "cpu_baseline": cpu,
     }

@@ -129,7 +129,7 @@ float ae_cosine_similarity(const float* a, const float* b);
 /* ---- operator level (device pointers, asynchronous on `stream`) ---------- */
 /* PackedLinearInt8::from_raw_row_major (src/gemm.rs:186-246): w_q [n_out,k_in]
  * row-major int8, w_scale/bias [n_out], inv_smooth [k_in] (host pointers).
- * Requires n_out % 128 == 0 and k_in % 64 == 0. */
+ * Requires n_out % 384 == 0 and k_in % 64 == 0. */
 int ae_linear_create(int n_out, int k_in, const int8_t* w_q, const float* w_scale,
                      const float* bias, const float* inv_smooth, ae_linear** out);
 void ae_linear_destroy(ae_linear* l);

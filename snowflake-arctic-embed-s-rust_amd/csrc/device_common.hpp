@@ -1,0 +1,128 @@
+// device_common.hpp -- exact scalar building blocks shared by the gfx950 kernels.
+//
+// Build flags that carry semantics: -ffp-contract=off (no a*b+c fusion: the
+// reference is Rust, which never contracts), correctly rounded f32 divide and
+// sqrt (HIP's default), no fast-math.  Every kernel evaluates exactly the
+// reference's scalar expression order (sequential sums, separately rounded
+// products, glibc's expf), so its outputs are bit-identical to the reference's
+// scalar backend on the same inputs, and so is the whole forward pass.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace aek {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int H = 384;
+constexpr int HQKV = 3 * 384;
+constexpr float kInvSqrtD = 0.17677669529663687f;  // 1.0f / sqrtf(32.0f), src/model.rs:222
+
+// ---------------------------------------------------------------------------
+// exact scalar building blocks
+// ---------------------------------------------------------------------------
+
+// `(v).round().clamp(-127.0, 127.0) as i8` (f32::round = half away from zero;
+// `as i8` maps NaN to 0).
+__device__ __forceinline__ int qround(float v) {
+  float r = roundf(v);
+  if (__builtin_isnan(r)) return 0;
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int)r;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// max(m, a) that ignores a NaN `a`, like `if a > max_abs { max_abs = a }`.
+__device__ __forceinline__ float nanless_max(float m, float a) { return a > m ? a : m; }
+
+// bits(2^(i/32) rounded to double) - (i << 47), i = 0..31: the exp2 table of
+// expf_libm below (computed from 2^(i/32) in quad precision).
+static __constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+// The table lives in registers across the wave: lane l keeps entry l % 32 as two
+// 32-bit halves, and a lookup is a pair of ds_bpermute (a crossbar read of
+// another lane's register: no LDS bank conflicts, unlike a data-dependent
+// ds_read of a shared table).  A lookup reads lanes 0..31, so EVERY lane of the
+// wave must be active at every expf_libm / gelu_exact call: call them only
+// from wave-uniform control flow.
+struct ExpTab {
+  uint32_t lo, hi;
+};
+
+__device__ __forceinline__ ExpTab exp_tab_regs() {
+  const uint64_t t = kExp2Tab[threadIdx.x & 31];
+  return ExpTab{(uint32_t)t, (uint32_t)(t >> 32)};
+}
+
+__device__ __forceinline__ uint64_t exp_tab_lookup(const ExpTab& tb, uint32_t i) {
+  const int addr = (int)(i << 2);  // byte address of lane i
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)tb.lo);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)tb.hi);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// expf as glibc computes it on x86_64 (sysdeps/ieee754/flt-32/e_expf.c, the
+// ARM optimized-routines design with a 32-entry 2^(i/32) table and a cubic
+// polynomial, evaluated in double with the FMA contractions of glibc's -mfma
+// build).  The reference's scalar GELU and softmax call f32::exp, i.e. this
+// function.  Verified equal to glibc expf on every float in [-104, -0]; valid
+// for x <= 0 and NaN.  Branch-free (see ExpTab): the underflow case of glibc,
+// x < log(2^-150), is applied as a final select.
+__device__ __forceinline__ float expf_libm(float x, const ExpTab& tb) {
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  const double kShift = 0x1.8p+52;
+  const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  const double xd = (double)x;
+  double kd = __builtin_fma(kInvLn2N, xd, kShift);
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= kShift;
+  const double r = __builtin_fma(kInvLn2N, xd, -kd);
+  const uint64_t t = exp_tab_lookup(tb, (uint32_t)ki & 31u) + (ki << 47);
+  const double s = __longlong_as_double((long long)t);
+  const double z = __builtin_fma(c0, r, c1);
+  const double r2 = r * r;
+  double y = __builtin_fma(c2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  const float res = (float)y;
+  return x < -0x1.9fe368p6f ? 0.0f : res;  // glibc's underflow branch
+}
+
+// scalar_gelu (reference src/simd_math.rs:15-23), same operation order.
+// Wave-uniform control flow required (see ExpTab).
+__device__ __forceinline__ float gelu_exact(float x, const ExpTab& tb) {
+  const float z = fabsf(x) * 0.70710677f;
+  const float t = 1.0f / (1.0f + 0.3275911f * z);
+  const float poly =
+      t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  const float erf_val = copysignf(1.0f - poly * expf_libm(-z * z, tb), x);
+  return 0.5f * x * (1.0f + erf_val);
+}
+
+// index of the segment containing token t: largest b with cu[b] <= t (cu has B+1 entries)
+__device__ __forceinline__ int find_segment(const int* cu, int B, int t) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace aek

@@ -67,20 +67,6 @@ int check_device(int* dev_out) {
   return AE_OK;
 }
 
-// [N,K] row-major int8 -> [N/128][K/64][128 rows][64 bytes] (one contiguous
-// 8 KiB tile per (128-column, 64-k) block of the GEMM)
-std::vector<int8_t> swizzle_weights(int n, int k, const int8_t* w) {
-  std::vector<int8_t> out(size_t(n) * k);
-  const int kt_n = k / 64;
-  for (int nt = 0; nt < n / 128; nt++)
-    for (int kt = 0; kt < kt_n; kt++) {
-      int8_t* dst = out.data() + (size_t(nt) * kt_n + kt) * 8192;
-      for (int r = 0; r < 128; r++)
-        std::memcpy(dst + r * 64, w + size_t(nt * 128 + r) * k + kt * 64, 64);
-    }
-  return out;
-}
-
 void free_all(std::vector<void*>& ptrs) {
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
@@ -110,11 +96,12 @@ struct ae_linear {
 namespace {
 int make_linear(int n, int k, const int8_t* w_q, const float* w_scale, const float* bias, const float* inv_smooth,
                 ae_linear* l) {
-  if (n <= 0 || k <= 0 || n % 128 || k % 64) return fail(AE_ERR_INVALID_ARG, "linear shape must be n%128==0, k%64==0");
+  if (n <= 0 || k <= 0 || n % 384 || k % 64) return fail(AE_ERR_INVALID_ARG, "linear shape must be n%384==0, k%64==0");
   l->n = n;
   l->k = k;
   l->owns = true;
-  std::vector<int8_t> sw = swizzle_weights(n, k, w_q);
+  std::vector<int8_t> sw(size_t(n) * k);
+  aek::swizzle_weights(n, k, w_q, sw.data());
   if (int rc = dupload(&l->w, sw.data(), sw.size())) return rc;
   if (int rc = dupload(&l->w_scale, w_scale, size_t(n))) return rc;
   if (int rc = dupload(&l->bias, bias, size_t(n))) return rc;

@@ -1,0 +1,218 @@
+// gemm.hip -- W8A8 int8 MFMA GEMM for gfx950 with the reference's fused epilogue.
+//
+//   out[m,n] = fma(f32(sum_k a[m,k]*w[n,k]), sa[m]*ws[n], bias[n] (+ res[m,n]))
+//
+// (gemm_scalar_fused, reference src/gemm.rs:2000-2029: integer accumulation,
+// then one f32 conversion, one product sa*ws, one sum bias+res and one fma.)
+//
+// Tiling: one workgroup = 4 waves = 64 rows x 384 columns; wave w owns columns
+// [w*96, w*96+96) as 4 x 6 tiles of v_mfma_i32_16x16x64_i8 (96 accumulator
+// VGPRs), K step 64.
+//  * A (64 x 64 int8 per step) is staged through LDS and shared by the 4 waves.
+//    Its global loads run two K steps ahead in registers; f32 A (the
+//    quantize-on-load variants) is converted to int8 only when it is written
+//    to LDS, so the load latency overlaps two steps of MFMA work.
+//  * Each wave streams its B fragments straight from global memory: W is
+//    pre-swizzled at load time into MFMA fragment order [K/64][N/16][64][16],
+//    so every fragment load is one coalesced 1 KiB transaction (one step ahead).
+//  * The epilogue stages each 16-row block of int32 accumulators through LDS
+//    and then walks whole rows with float4 accesses, so outputs and residuals
+//    move as full 128-byte lines.
+// For the N = 384 GEMMs (attn_out, FFN-down) one workgroup spans the whole row,
+// so f32 A rows are read and quantized exactly once.
+//
+// MFMA operand layout (16x16x64 i8): lane l supplies row (l%16) of A and column
+// (l%16) of B, 16 k-values from k-group (l/16); A and B share that k order, so the
+// integer sum is exact.  Output: lane l, register r holds D[4*(l/16)+r][l%16].
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aek {
+
+constexpr int kBM = 64;      // rows per workgroup
+constexpr int kBN = 384;     // columns per workgroup
+constexpr int kWaveN = 96;   // columns per wave
+constexpr int kCB = kWaveN / 16;
+constexpr int kAPitch = 80;  // LDS row pitch of the A tile (bytes): conflict-free fragment reads
+constexpr int kEPitch = 100; // LDS row pitch of the epilogue staging tile (words)
+
+template <int AM>
+struct ARegs;
+template <>
+struct ARegs<kAI8> {
+  v4i v;
+};
+template <int AM>
+struct ARegs {
+  float4 v[4];
+};
+
+template <int AM, int EM>
+__global__ __launch_bounds__(256, 2) void gemm_w8a8_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(16))) int8_t sA[2][kBM * kAPitch];
+  __shared__ __attribute__((aligned(16))) int sE[4][16 * kEPitch];  // per-wave epilogue staging
+  __shared__ uint32_t sRowMax[4][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;  // M tiles on x (y is limited to 65536)
+  const int KT = p.K >> 6;
+  const int NB = p.N >> 4;  // 16-column fragments per K step in the swizzled W
+  const ExpTab tb = exp_tab_regs();  // the epilogue loop below is wave-uniform
+
+  // A loader: 4 threads per row, 16 k-values each
+  const int lrow = tid >> 2, lpart = tid & 3;
+  const int arow = min(m0 + lrow, p.M - 1);
+  float a_inv = 0.0f;
+  if (AM != kAI8) a_inv = 127.0f / __uint_as_float(p.a_rowmax[arow]);  // inv_scale = 127.0 / max_abs
+  auto aload = [&](int kt, ARegs<AM>& r) {
+    const int kb = kt * 64 + lpart * 16;
+    if constexpr (AM == kAI8) {
+      r.v = *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(p.A) + (size_t)arow * p.K + kb);
+    } else {
+      const float4* src = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.A) + (size_t)arow * p.K + kb);
+#pragma unroll
+      for (int i = 0; i < 4; i++) r.v[i] = src[i];
+    }
+  };
+  auto astore = [&](int kt, int buf, const ARegs<AM>& r) {
+    v4i q;
+    if constexpr (AM == kAI8) {
+      q = r.v;
+    } else {
+      const int kb = kt * 64 + lpart * 16;
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float4 x = r.v[i];
+        if (AM == kAF32QSmooth) {  // (x * inv_smooth[j]) * inv_scale
+          const float4 s = reinterpret_cast<const float4*>(p.a_smooth + kb)[i];
+          x.x = x.x * s.x; x.y = x.y * s.y; x.z = x.z * s.z; x.w = x.w * s.w;
+        }
+        w[i] = pack4(qround(x.x * a_inv), qround(x.y * a_inv), qround(x.z * a_inv), qround(x.w * a_inv));
+      }
+      q = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+    *reinterpret_cast<v4i*>(&sA[buf][lrow * kAPitch + lpart * 16]) = q;
+  };
+  // B fragments of this wave for one K step
+  const int cb0 = (n0 + wave * kWaveN) >> 4;
+  const int8_t* wbase = p.w + (size_t)lane * 16;
+  v4i bcur[kCB], bnext[kCB];
+  auto bload = [&](int kt, v4i* dst) {
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+      dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + cb0 + j) * 1024);
+  };
+
+  v4i acc[4][kCB];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < kCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+  ARegs<AM> r1, r2;  // A for steps kt+1 and kt+2
+  {
+    ARegs<AM> r0;
+    aload(0, r0);
+    if (KT > 1) aload(1, r1);
+    bload(0, bcur);
+    astore(0, 0, r0);
+  }
+  __syncthreads();
+  const int fr = lane & 15, fk = (lane >> 4) * 16;
+  for (int kt = 0; kt < KT; kt++) {
+    const int buf = kt & 1;
+    if (kt + 2 < KT) aload(kt + 2, r2);
+    if (kt + 1 < KT) bload(kt + 1, bnext);
+    v4i af[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[buf][(i * 16 + fr) * kAPitch + fk]);
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bcur[j], acc[i][j], 0, 0, 0);
+    if (kt + 1 < KT) astore(kt + 1, buf ^ 1, r1);
+    __syncthreads();
+    if (kt + 1 < KT) {
+#pragma unroll
+      for (int j = 0; j < kCB; j++) bcur[j] = bnext[j];
+      r1 = r2;
+    }
+  }
+
+  // epilogue, one 16-row block at a time through this wave's LDS tile:
+  // accumulators -> sE[16][96] (int32), then lanes walk rows with float4s
+  int* E = sE[wave];
+  const int col0 = n0 + wave * kWaveN;  // first column of this wave
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
+    if (EM == kEpiGelu && lane < 16) sRowMax[wave][lane] = 0u;
+    __syncthreads();  // (wave-local data; also orders sRowMax resets)
+#pragma unroll
+    for (int k = 0; k < 6; k++) {  // 16 rows x 24 float4 = 384 = 6 per lane
+      const int idx = lane + 64 * k, rr = idx / 24, c4 = idx % 24;
+      const int row = m0 + i * 16 + rr;
+      const bool ok = row < p.M;
+      const int rrow = ok ? row : p.M - 1;
+      const int col = col0 + c4 * 4;
+      float sa;
+      if (AM == kAI8) sa = p.a_scale[rrow];
+      else sa = __uint_as_float(p.a_rowmax[rrow]) / 127.0f;  // scale = max_abs / 127.0
+      const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
+      const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
+      float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
+      if (p.res) {
+        const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)rrow * p.N + col);
+        b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+      }
+      float4 v;
+      v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
+      v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
+      v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
+      v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
+      if (EM == kEpiGelu) {
+        const float4 g4 = *reinterpret_cast<const float4*>(p.g_smooth + col);
+        v.x = gelu_exact(v.x, tb) * g4.x;
+        v.y = gelu_exact(v.y, tb) * g4.y;
+        v.z = gelu_exact(v.z, tb) * g4.z;
+        v.w = gelu_exact(v.w, tb) * g4.w;
+        float gm = nanless_max(nanless_max(fabsf(v.x), fabsf(v.y)), nanless_max(fabsf(v.z), fabsf(v.w)));
+        atomicMax(&sRowMax[wave][rr], __float_as_uint(gm));  // non-negative f32 bits order like u32
+      }
+      if (ok) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
+    }
+    __syncthreads();
+    if (EM == kEpiGelu && lane < 16) {
+      const int row = m0 + i * 16 + lane;
+      if (row < p.M) atomicMax(&p.g_rowmax[row], sRowMax[wave][lane]);
+    }
+  }
+}
+
+void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st) {
+  dim3 grid((p.M + kBM - 1) / kBM, p.N / kBN);
+  if (amode == kAI8 && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiF32>), grid, dim3(256), 0, st, p);
+  else if (amode == kAI8 && emode == kEpiGelu) hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiGelu>), grid, dim3(256), 0, st, p);
+  else if (amode == kAF32Q && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32Q, kEpiF32>), grid, dim3(256), 0, st, p);
+  else if (amode == kAF32QSmooth && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32QSmooth, kEpiF32>), grid, dim3(256), 0, st, p);
+}
+
+// [N,K] row-major int8 -> [K/64][N/16][64 lanes][16 bytes]: lane l of fragment
+// (kt, cb) holds w[cb*16 + l%16][kt*64 + (l/16)*16 .. +16]
+void swizzle_weights(int n, int k, const int8_t* w, int8_t* out) {
+  const int nb = n / 16;
+  for (int kt = 0; kt < k / 64; kt++)
+    for (int cb = 0; cb < nb; cb++)
+      for (int l = 0; l < 64; l++) {
+        const int8_t* src = w + (size_t)(cb * 16 + (l & 15)) * k + kt * 64 + (l >> 4) * 16;
+        int8_t* dst = out + (((size_t)kt * nb + cb) * 64 + l) * 16;
+        for (int b = 0; b < 16; b++) dst[b] = src[b];
+      }
+}
+
+}  // namespace aek

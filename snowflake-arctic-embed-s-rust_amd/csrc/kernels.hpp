@@ -21,7 +21,7 @@ struct GemmArgs {
   const float* a_scale;       // kAI8: [M]
   const uint32_t* a_rowmax;   // kAF32Q*: [M] bits of max_abs (>= 1e-8)
   const float* a_smooth;      // kAF32QSmooth: inv_smooth [K]
-  const int8_t* w;            // pre-swizzled [N/128][K/64][128][64]
+  const int8_t* w;            // pre-swizzled by swizzle_weights
   const float* w_scale;       // [N]
   const float* bias;          // [N]
   const float* res;           // [M,N] or null
@@ -29,7 +29,10 @@ struct GemmArgs {
   const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
   uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
 };
+// N % 384 == 0, K % 64 == 0
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
+// host: [N,K] row-major int8 -> the GEMM's fragment order [K/64][N/16][64][16] (out has N*K bytes)
+void swizzle_weights(int n, int k, const int8_t* w, int8_t* out);
 
 constexpr int kLnSrcF32 = 0;
 constexpr int kLnSrcEmb = 1;

@@ -1,0 +1,234 @@
+// rowops.hip -- row-wise kernels of the encoder: embedding gather + LayerNorm +
+// SmoothQuant + int8 quantization, the stand-alone quantizers, and the final
+// LayerNorm + L2 normalization of the [CLS] rows.
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aek {
+
+// ---------------------------------------------------------------------------
+// LayerNorm + SmoothQuant + dynamic int8 quantization over 384-wide rows
+// (layernorm_smooth_quantize_row_scalar, reference src/simd_math.rs:208-247).
+//
+// WG = 256 threads, 32 rows.  Phase A stages x into LDS; phase B gives each
+// row to one lane, which forms the mean and variance with the reference's
+// sequential left-to-right sums; phase C normalizes, takes the order-free row
+// absmax and quantizes with 8 lanes per row.  Source modes: f32 rows, or the
+// embedding gather ((w*ws + p*ps) + type0, src/simd_math.rs:1877-1880).
+// ---------------------------------------------------------------------------
+constexpr int kLnRows = 32;
+constexpr int kLnPitch = 388;
+
+template <int SRC>
+__global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
+  __shared__ __attribute__((aligned(16))) float tile[kLnRows * kLnPitch];
+  __shared__ float s_mean[kLnRows], s_rstd[kLnRows];
+  const int tid = threadIdx.x, rl = tid >> 3, sub = tid & 7;
+  const int row = blockIdx.x * kLnRows + rl;
+  const bool valid = row < p.T;
+  const int rrow = valid ? row : p.T - 1;
+
+  float4 xv[12];
+  if (SRC == kLnSrcEmb) {
+    // ids and positions are validated on the host; the clamps keep a malformed
+    // device-resident batch inside the tables
+    const int tok = min((int)p.ids[rrow], 30522 - 1);
+    const int seg = find_segment(p.cu, p.B, rrow);
+    const int pos = max(0, min(rrow - p.cu[seg], 512 - 1));
+    const float ws = p.word_s[tok], ps = p.pos_s[pos];
+    const int8_t* wr = p.word_q + (size_t)tok * H;
+    const int8_t* pr = p.pos_q + (size_t)pos * H;
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = (sub + 8 * i) * 4;
+      const uint32_t wv = *reinterpret_cast<const uint32_t*>(wr + c);
+      const uint32_t pv = *reinterpret_cast<const uint32_t*>(pr + c);
+      const float4 t = *reinterpret_cast<const float4*>(p.type0 + c);
+      float x[4];
+      const float tt[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float w = (float)(int8_t)(wv >> (8 * k));
+        const float q = (float)(int8_t)(pv >> (8 * k));
+        x[k] = w * ws + q * ps + tt[k];
+      }
+      xv[i] = make_float4(x[0], x[1], x[2], x[3]);
+    }
+  } else {
+    const float4* src = reinterpret_cast<const float4*>(p.src + (size_t)rrow * H);
+#pragma unroll
+    for (int i = 0; i < 12; i++) xv[i] = src[sub + 8 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < 12; i++) *reinterpret_cast<float4*>(&tile[rl * kLnPitch + (sub + 8 * i) * 4]) = xv[i];
+  __syncthreads();
+
+  if (tid < kLnRows) {
+    const float* xr = &tile[tid * kLnPitch];
+    float sum = 0.0f;
+    for (int j = 0; j < H; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + j);
+      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    }
+    const float mean = sum / 384.0f;
+    float var_sum = 0.0f;
+    for (int j = 0; j < H; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + j);
+      float d;
+      d = v.x - mean; var_sum += d * d;
+      d = v.y - mean; var_sum += d * d;
+      d = v.z - mean; var_sum += d * d;
+      d = v.w - mean; var_sum += d * d;
+    }
+    s_mean[tid] = mean;
+    s_rstd[tid] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
+  }
+  __syncthreads();
+
+  const float mean = s_mean[rl], rstd = s_rstd[rl];
+  float amax = 0.0f;
+  float4 ys[12];
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    const int c = (sub + 8 * i) * 4;
+    const float4 g = *reinterpret_cast<const float4*>(p.gamma + c);
+    const float4 b = *reinterpret_cast<const float4*>(p.beta + c);
+    const float4 s = *reinterpret_cast<const float4*>(p.smooth + c);
+    float4 y;
+    y.x = (xv[i].x - mean) * rstd * g.x + b.x;
+    y.y = (xv[i].y - mean) * rstd * g.y + b.y;
+    y.z = (xv[i].z - mean) * rstd * g.z + b.z;
+    y.w = (xv[i].w - mean) * rstd * g.w + b.w;
+    if (valid) *reinterpret_cast<float4*>(p.dst + (size_t)row * H + c) = y;
+    ys[i] = make_float4(y.x * s.x, y.y * s.y, y.z * s.z, y.w * s.w);
+    amax = nanless_max(amax, fabsf(ys[i].x));
+    amax = nanless_max(amax, fabsf(ys[i].y));
+    amax = nanless_max(amax, fabsf(ys[i].z));
+    amax = nanless_max(amax, fabsf(ys[i].w));
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+  const float max_abs = nanless_max(1e-8f, amax);
+  const float inv_scale = 127.0f / max_abs;
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = (sub + 8 * i) * 4;
+      *reinterpret_cast<uint32_t*>(p.q + (size_t)row * H + c) =
+          pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale), qround(ys[i].z * inv_scale),
+                qround(ys[i].w * inv_scale));
+    }
+    if (sub == 0) {
+      p.scale[row] = max_abs / 127.0f;
+      if (p.rowmax_init) p.rowmax_init[row] = __float_as_uint(1e-8f);
+      if (p.rowmax_init2) p.rowmax_init2[row] = __float_as_uint(1e-8f);
+    }
+  }
+}
+
+void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st) {
+  dim3 grid((p.T + kLnRows - 1) / kLnRows);
+  if (src_mode == kLnSrcEmb) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32>), grid, dim3(256), 0, st, p);
+}
+
+// ---------------------------------------------------------------------------
+// Stand-alone row quantizers (operator-level API): one wave per row.
+// smooth_quantize_row (src/simd_math.rs:513-530), gelu_smooth_quantize_row
+// (src/simd_math.rs:1295-1312).
+// ---------------------------------------------------------------------------
+template <bool GELU>
+__global__ __launch_bounds__(256) void row_quant_kernel(int m, int n, float* x, const float* smooth, int8_t* q,
+                                                        float* scale) {
+  const ExpTab tb = exp_tab_regs();
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= m) return;
+  float* xr = x + (size_t)row * n;
+  float amax = 0.0f;
+  for (int j0 = 0; j0 < n; j0 += 64) {  // wave-uniform trip count (gelu_exact needs all lanes)
+    const int j = j0 + lane;
+    const bool in = j < n;
+    float v = in ? xr[j] : 0.0f;
+    if (GELU) {
+      v = gelu_exact(v, tb) * (in ? smooth[j] : 0.0f);
+      if (in) xr[j] = v;
+    } else if (in) {
+      v = v * smooth[j];
+    }
+    if (in) amax = nanless_max(amax, fabsf(v));
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+  const float max_abs = nanless_max(1e-8f, amax);
+  const float inv_scale = 127.0f / max_abs;
+  for (int j = lane; j < n; j += 64) {
+    const float v = GELU ? xr[j] * inv_scale : xr[j] * smooth[j] * inv_scale;
+    q[(size_t)row * n + j] = (int8_t)qround(v);
+  }
+  if (lane == 0) scale[row] = max_abs / 127.0f;
+}
+
+void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, float* scale, bool gelu,
+                      hipStream_t st) {
+  dim3 grid((m + 3) / 4);
+  if (gelu) hipLaunchKernelGGL((row_quant_kernel<true>), grid, dim3(256), 0, st, m, n, x, smooth, q, scale);
+  else hipLaunchKernelGGL((row_quant_kernel<false>), grid, dim3(256), 0, st, m, n, x, smooth, q, scale);
+}
+
+// final LayerNorm (no quantization, src/simd_math.rs:481-497) and L2 normalize
+// (src/simd_math.rs:2892-2903), one lane per row, sequential sums
+__global__ __launch_bounds__(64) void final_ln_l2_kernel(int B, const float* src, const float* gamma,
+                                                         const float* beta, float* out) {
+  const int b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= B) return;
+  const float* x = src + (size_t)b * H;
+  float* y = out + (size_t)b * H;
+  float sum = 0.0f;
+  for (int j = 0; j < H; j++) sum += x[j];
+  const float mean = sum / 384.0f;
+  float var_sum = 0.0f;
+  for (int j = 0; j < H; j++) {
+    const float d = x[j] - mean;
+    var_sum += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
+  float sum_sq = 0.0f;
+  for (int j = 0; j < H; j++) {
+    const float v = (x[j] - mean) * rstd * gamma[j] + beta[j];
+    y[j] = v;
+    sum_sq += v * v;
+  }
+  if (sum_sq > 0.0f) {
+    const float inv_norm = 1.0f / sqrtf(sum_sq);
+    for (int j = 0; j < H; j++) y[j] = y[j] * inv_norm;
+  }
+}
+
+void launch_final_ln_l2(int B, const float* src, const float* gamma, const float* beta, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(final_ln_l2_kernel, dim3((B + 63) / 64), dim3(64), 0, st, B, src, gamma, beta, out);
+}
+
+// fills a u32 buffer (row-absmax initial values, bits of 1e-8f)
+__global__ void fill_u32_kernel(uint32_t* dst, int n, uint32_t v) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = v;
+}
+void launch_fill_u32(uint32_t* dst, int n, uint32_t v, hipStream_t st) {
+  if (n > 0) hipLaunchKernelGGL(fill_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, dst, n, v);
+}
+
+// exact GELU elementwise (test hook for exhaustive checks)
+__global__ void gelu_map_kernel(const float* x, float* y, size_t n) {
+  const ExpTab tb = exp_tab_regs();
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const float v = gelu_exact(i < n ? x[i] : 0.0f, tb);  // every lane evaluates (see ExpTab)
+  if (i < n) y[i] = v;
+}
+void launch_gelu_map(const float* x, float* y, size_t n, hipStream_t st) {
+  if (n > 0) hipLaunchKernelGGL(gelu_map_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, y, n);
+}
+
+}  // namespace aek

@@ -54,7 +54,7 @@ def test_gemm_bit_exact(torch_gpu, n, k, m, with_res):
 
 def test_gemm_extreme_accumulators(torch_gpu):
     torch = torch_gpu
-    n, k, m = 128, 1536, 3
+    n, k, m = 384, 1536, 3
     w = np.full((n, k), 127, np.int8)
     w[1::2] = -127
     a = np.full((m, k), 127, np.int8)
