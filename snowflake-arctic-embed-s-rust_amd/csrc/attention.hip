@@ -17,233 +17,416 @@ namespace aek {
 //   ctx_d = sum_{t in order} p_t * v_t,d
 // every sum left to right with separately rounded products.
 //
-// WG (tile, head) owns kAttnQ queries of one sequence.  Scores for all keys of
-// the sequence stay in LDS (row pitch = padded max length); the score, exp and
-// PV phases use all 256 lanes, only the in-order softmax denominator is one
-// lane per query.  tile_start[b] = sum_{b'<b} ceil(L_b'/kAttnQ) is built on the
-// device from cu_seqlens.  Also folds the SmoothQuant row absmax of the output
-// (|ctx_j * inv_smooth_j|) into `rowmax` (atomicMax on non-negative f32 bits),
-// which the attn_out GEMM prologue consumes.
+// Segments longer than kAttnShortMax: a WG (tile, head) owns kAttnQ queries of
+// one sequence.  Scores for all keys of the sequence stay in LDS (row pitch =
+// padded max length); the score, exp and PV phases use all 256 lanes, only the
+// in-order softmax denominator is one lane per query.  Shorter segments go to
+// attention_short_kernel (one wave per segment and head).  Both fold the
+// SmoothQuant row absmax of the output (|ctx_j * inv_smooth_j|) into `rowmax`
+// (atomicMax on non-negative f32 bits), which the attn_out GEMM prologue
+// consumes.
 // ---------------------------------------------------------------------------
 constexpr int kAttnQ = 32;     // queries per workgroup
-constexpr int kKeyChunk = 64;  // keys per K/V staging chunk
-constexpr int kKPitch = 36;    // K chunk row pitch (floats): conflict-free 16-byte reads
 
-__global__ __launch_bounds__(256) void tile_starts_kernel(const int* cu, int B, int* tile_start) {
-  __shared__ int part[256];
+// Work plan, built on the device from cu_seqlens: segments of 1..kAttnShortMax
+// tokens go to the short kernel (plan[B+1] = their count, plan[B+2..] = their
+// indices in order); longer ones to the tiled kernel, which finds its segment
+// from plan[b] = sum_{b'<b} long tiles of b' (plan[B] = total).
+__device__ __forceinline__ int long_tiles(int L) { return L > kAttnShortMax ? (L + kAttnQ - 1) / kAttnQ : 0; }
+__device__ __forceinline__ int is_short(int L) { return L >= 1 && L <= kAttnShortMax ? 1 : 0; }
+
+__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int* plan) {
+  __shared__ int part_t[256], part_s[256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
-  int s = 0;
-  for (int b = b0; b < b1; b++) s += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
-  part[tid] = s;
+  int nt = 0, ns = 0;
+  for (int b = b0; b < b1; b++) {
+    const int L = cu[b + 1] - cu[b];
+    nt += long_tiles(L);
+    ns += is_short(L);
+  }
+  part_t[tid] = nt;
+  part_s[tid] = ns;
   __syncthreads();
   if (tid == 0) {
-    int acc = 0;
+    int at = 0, as = 0;
     for (int i = 0; i < 256; i++) {
-      int v = part[i];
-      part[i] = acc;
-      acc += v;
+      const int vt = part_t[i], vs = part_s[i];
+      part_t[i] = at;
+      part_s[i] = as;
+      at += vt;
+      as += vs;
     }
+    plan[B] = at;
+    plan[B + 1] = as;
   }
   __syncthreads();
-  int acc = part[tid];
+  int at = part_t[tid], as = part_s[tid];
+  int* short_list = plan + B + 2;
   for (int b = b0; b < b1; b++) {
-    tile_start[b] = acc;
-    acc += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
+    const int L = cu[b + 1] - cu[b];
+    plan[b] = at;
+    at += long_tiles(L);
+    if (is_short(L)) short_list[as++] = b;
   }
-  if (b1 == B && b0 < b1) tile_start[B] = acc;
-  if (B == 0 && tid == 0) tile_start[0] = 0;
 }
 
-// dynamic LDS: S[kAttnQ][s_pitch] scores/probabilities, then K/V chunk, Q tile
+// ---------------------------------------------------------------------------
+// Short segments (1..64 tokens): one wave per (segment, head), lane = query.
+// Each lane runs the reference's scalar sequence for its own query row
+// (scores, max, exp with the in-order sum, normalise, in-order PV) over its own
+// LDS row, so no barrier is needed.  The K and V rows are the same for every
+// lane: they are read once per wave through the scalar data cache (constant
+// address space, uniform addresses) into two ping-pong register sets, one key
+// ahead of their use, and enter the VALU as scalar operands.
+// ---------------------------------------------------------------------------
+constexpr int kShortPitch = kAttnShortMax + 4;  // LDS floats per lane row (16-byte aligned rows)
+
+typedef const float __attribute__((address_space(4)))* uniform_fptr;
+
+__device__ __forceinline__ uniform_fptr as_uniform(const float* p) { return (uniform_fptr)(uintptr_t)p; }
+
+__device__ __forceinline__ void load_row32(uniform_fptr r, float (&x)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; i++) x[i] = r[i];
+}
+
+// dot32_f32 scalar order (src/simd_math.rs:1461-1468), times 1/sqrt(32)
+__device__ __forceinline__ float score32(const float (&q)[32], const float (&k)[32]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) acc += q[i] * k[i];
+  return acc * kInvSqrtD;
+}
+
+__device__ __forceinline__ void pv_step(float (&o)[32], float pt, const float (&v)[32]) {
+#pragma unroll
+  for (int d = 0; d < 32; d++) o[d] = o[d] + pt * v[d];
+}
+
+__global__ __launch_bounds__(64) void attention_short_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(16))) float S[64 * kShortPitch];
+  const int* short_list = p.plan + p.B + 1;  // [0] = count
+  const int item = blockIdx.x, h = blockIdx.y;
+  if (item >= short_list[0]) return;
+  const int b = short_list[1 + item];
+  const int s0 = p.cu[b];
+  const int L = p.cu[b + 1] - s0;  // 1..kAttnShortMax (the plan guarantees it)
+  const int lane = threadIdx.x;
+  const ExpTab tb = exp_tab_regs();
+  float* row = S + lane * kShortPitch;
+  const int qi = min(lane, L - 1);  // lanes past the segment repeat its last query; never stored
+  float q[32];
+#pragma unroll
+  for (int c = 0; c < 32; c += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + qi) * HQKV + h * 32 + c);
+    q[c] = v.x; q[c + 1] = v.y; q[c + 2] = v.z; q[c + 3] = v.w;
+  }
+  const uniform_fptr kbase = as_uniform(p.qkv + (size_t)s0 * HQKV + H + h * 32);
+  const uniform_fptr vbase = as_uniform(p.qkv + (size_t)s0 * HQKV + 2 * H + h * 32);
+  const int last = L - 1;
+
+  // scores and row max; keys in pairs (A, B), the prefetched row clamped to the segment
+  float ka[32], kb[32];
+  float m = -INFINITY;
+  load_row32(kbase, ka);
+  int t = 0;
+  for (; t + 1 < L; t += 2) {
+    load_row32(kbase + (t + 1) * HQKV, kb);
+    const float sa = score32(q, ka);
+    load_row32(kbase + min(t + 2, last) * HQKV, ka);
+    const float sb = score32(q, kb);
+    row[t] = sa;
+    row[t + 1] = sb;
+    m = nanless_max(nanless_max(m, sa), sb);
+  }
+  if (t < L) {  // odd length: key L-1 is in ka
+    const float sa = score32(q, ka);
+    row[t] = sa;
+    m = nanless_max(m, sa);
+  }
+  // e_t = expf(s_t - max) with the in-order sum, 4 keys per LDS access (entries
+  // past L are pitch padding: their exps are discarded and add nothing)
+  float sum = 0.0f;
+  for (int t4 = 0; t4 < L; t4 += 4) {
+    float4 v = *reinterpret_cast<const float4*>(row + t4);
+    v.x = expf_libm(v.x - m, tb);
+    v.y = expf_libm(v.y - m, tb);
+    v.z = expf_libm(v.z - m, tb);
+    v.w = expf_libm(v.w - m, tb);
+    *reinterpret_cast<float4*>(row + t4) = v;
+    sum += v.x;
+    if (t4 + 1 < L) sum += v.y;
+    if (t4 + 2 < L) sum += v.z;
+    if (t4 + 3 < L) sum += v.w;
+  }
+  const float inv = 1.0f / sum;
+  // ctx_d = sum_t (e_t * inv) * v_t,d in order
+  float o[32];
+#pragma unroll
+  for (int d = 0; d < 32; d++) o[d] = 0.0f;
+  load_row32(vbase, ka);
+  t = 0;
+  for (; t + 1 < L; t += 2) {
+    load_row32(vbase + (t + 1) * HQKV, kb);
+    const float2 e2 = *reinterpret_cast<const float2*>(row + t);
+    pv_step(o, e2.x * inv, ka);
+    load_row32(vbase + min(t + 2, last) * HQKV, ka);
+    pv_step(o, e2.y * inv, kb);
+  }
+  if (t < L) pv_step(o, row[t] * inv, ka);
+
+  if (lane < L) {
+    float* dst = p.ctx + (size_t)(s0 + lane) * H + h * 32;
+#pragma unroll
+    for (int d = 0; d < 32; d += 4) *reinterpret_cast<float4*>(dst + d) = make_float4(o[d], o[d + 1], o[d + 2], o[d + 3]);
+    if (p.rowmax) {
+      float a = 0.0f;
+#pragma unroll
+      for (int d = 0; d < 32; d++) a = nanless_max(a, fabsf(o[d] * p.smooth[h * 32 + d]));
+      atomicMax(&p.rowmax[s0 + lane], __float_as_uint(a));
+    }
+  }
+}
+
+// MFMA as an exact multiplier.  v_mfma_f32_16x16x1_4b_f32 with a zero
+// accumulator returns the correctly rounded f32 product a*b for each of its
+// 4 x 16 x 16 outputs (K = 1: one product per output, rounded once), i.e. the
+// same value as the VALU's v_mul_f32, up to the sign of an exact zero, which
+// cannot change a sum that starts at +0.  The matrix core thus takes every
+// multiply of QK^T and PV; the VALU keeps the separately rounded, in-order
+// additions the reference's scalar loops perform.  Operand/result layout (lane l,
+// result register r): A[m][blk] from lane blk*16 + m, B[n][blk] from lane
+// blk*16 + n; result r holds block r/4, row m = 4*(l/16) + r%4, column n = l%16.
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f mfma_products(float a, float b) {
+  const v16f zero = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, zero, 0, 0, 0);
+}
+
+// acc[i] += blocks 0..3 of `pr` in block order (the blocks are consecutive
+// terms of the reference's sums)
+__device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
+#pragma unroll
+  for (int blk = 0; blk < 4; blk++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + pr[4 * blk + i];
+}
+
+// dynamic LDS: S[kAttnQ][s_pitch] scores -> exps, s_pitch = round16(max length) + 4
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  __shared__ float s_inv[kAttnQ];
+  __shared__ float s_maxw[4][kAttnQ];
+  __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
   const int tile = blockIdx.x, h = blockIdx.y;
-  if (tile >= p.tile_start[p.B]) return;
+  const int* tile_start = p.plan;
+  if (tile >= tile_start[p.B]) return;
   int lo = 0, hi = p.B - 1;
   while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (p.tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
   }
   const int b = lo;
   const int s0 = p.cu[b];
-  const int L = min(p.cu[b + 1] - s0, p.s_pitch - 4);  // the host sizes s_pitch >= L + 4
-  const int q0 = (tile - p.tile_start[b]) * kAttnQ;
-  const int nq = min(kAttnQ, L - q0);
   const int pitch = p.s_pitch;
-  float* S = smem;                                   // [kAttnQ][pitch]
-  float* KV = smem + kAttnQ * pitch;                 // [kKeyChunk][kKPitch]
-  float* Qs = KV + kKeyChunk * kKPitch;              // [kAttnQ][32]
-  const int tid = threadIdx.x;
+  const int L = min(p.cu[b + 1] - s0, pitch - 4);  // the host sizes pitch >= round16(L) + 4
+  const int q0 = (tile - tile_start[b]) * kAttnQ;
+  const int nq = min(kAttnQ, L - q0);
+  const int nqh = (nq + 15) >> 4;  // query halves with at least one query
+  float* S = smem;                 // [kAttnQ][pitch]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;  // fragment row / block of this lane
   const ExpTab tb = exp_tab_regs();
-  {  // Q tile (rows past the segment are clamped; their results are never stored)
-    const int r = tid >> 3, c4 = tid & 7;
-    const int qr = min(q0 + r, L - 1);
-    *reinterpret_cast<float4*>(&Qs[r * 32 + c4 * 4]) =
-        *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + qr) * HQKV + h * 32 + c4 * 4);
+  const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
+
+  // Q fragments: qf[qh][j] = Q[q0 + 16qh + lr][4j + lg] (rows past the segment clamped)
+  float qf[2][8];
+#pragma unroll
+  for (int qh = 0; qh < 2; qh++) {
+    const int qr = min(q0 + 16 * qh + lr, L - 1);
+#pragma unroll
+    for (int j = 0; j < 8; j++) qf[qh][j] = qkv[(size_t)qr * HQKV + 4 * j + lg];
   }
 
-  // phase 1: scores.  thread -> 2 queries (held in registers) x 4 keys of each
-  // 64-key chunk: 8 independent dot chains, each summed in order i = 0..31
-  // (dot32_f32 scalar branch: separately rounded products, sequential adds).
-  // Keys kq + 16j: the 4 rows one wave reads per instruction fall in distinct
-  // LDS bank groups.
-  const int qa = 2 * (tid & 15), kq = tid >> 4;
+  // phase 1: scores (dot32_f32 scalar order) and the row max.  Wave w takes the
+  // 16-key blocks kb = w, w+4, ... with both query halves; A = K block, B = Q
+  // half, so lane l ends with the scores of query 16qh + lr for keys
+  // 16kb + 4lg + i.  K fragments come straight from global memory (L2), one
+  // block ahead, into ping-pong registers (rows clamped to the segment).
+  // The row max uses v_max_f32 (fmaxf): it ignores NaN like the reference's
+  // `if s > max` scan, and the sign it gives an all-zero max cannot change
+  // expf(s - max).
+  float mrow[2] = {-INFINITY, -INFINITY};
+  const int nkb = (L + 15) >> 4;
+  const float* kcol = qkv + H + lg;
+  auto load_kf = [&](int kb, float (&kf)[8]) {
+    const float* src = kcol + (size_t)min(16 * kb + lr, L - 1) * HQKV;
+#pragma unroll
+    for (int j = 0; j < 8; j++) kf[j] = src[4 * j];
+  };
+  auto score_half = [&](int t, const float (&kf)[8], const float (&q)[8], float* srow, float& m) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; j++) add_blocks(acc, mfma_products(kf[j], q[j]));
+    float4 sc;
+    sc.x = acc[0] * kInvSqrtD;
+    sc.y = acc[1] * kInvSqrtD;
+    sc.z = acc[2] * kInvSqrtD;
+    sc.w = acc[3] * kInvSqrtD;
+    *reinterpret_cast<float4*>(srow + t) = sc;  // t + 3 < round16(L) <= pitch - 4
+    if (t + 3 < L) {
+      m = fmaxf(fmaxf(m, sc.x), fmaxf(sc.y, fmaxf(sc.z, sc.w)));
+    } else {
+      if (t < L) m = fmaxf(m, sc.x);
+      if (t + 1 < L) m = fmaxf(m, sc.y);
+      if (t + 2 < L) m = fmaxf(m, sc.z);
+    }
+  };
+  float* srow0 = &S[lr * pitch];
+  float* srow1 = &S[(16 + lr) * pitch];
+  auto score_block = [&](int kb, const float (&kf)[8]) {
+    const int t = 16 * kb + 4 * lg;
+    score_half(t, kf, qf[0], srow0, mrow[0]);
+    if (nqh > 1) score_half(t, kf, qf[1], srow1, mrow[1]);  // wave-uniform
+  };
+  {
+    float ka[8], kb8[8];
+    if (wave < nkb) load_kf(wave, ka);
+    for (int kb = wave; kb < nkb; kb += 8) {  // wave-uniform
+      load_kf(kb + 4, kb8);
+      score_block(kb, ka);
+      if (kb + 4 >= nkb) break;
+      load_kf(kb + 8, ka);
+      score_block(kb + 4, kb8);
+    }
+  }
+#pragma unroll
+  for (int qh = 0; qh < 2; qh++) {
+    float m = mrow[qh];
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (lane < 16) s_maxw[wave][16 * qh + lane] = m;
+  }
   __syncthreads();
-  float qv0[32], qv1[32];
-#pragma unroll
-  for (int c = 0; c < 32; c += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(&Qs[qa * 32 + c]);
-    const float4 bq = *reinterpret_cast<const float4*>(&Qs[(qa + 1) * 32 + c]);
-    qv0[c] = a.x; qv0[c + 1] = a.y; qv0[c + 2] = a.z; qv0[c + 3] = a.w;
-    qv1[c] = bq.x; qv1[c + 1] = bq.y; qv1[c + 2] = bq.z; qv1[c + 3] = bq.w;
-  }
-  for (int k0 = 0; k0 < L; k0 += kKeyChunk) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int idx = tid + i * 256, key = idx >> 3, c4 = idx & 7;
-      const int kr = min(k0 + key, L - 1);
-      *reinterpret_cast<float4*>(&KV[key * kKPitch + c4 * 4]) =
-          *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + kr) * HQKV + H + h * 32 + c4 * 4);
-    }
-    __syncthreads();
-    float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < 32; c += 4) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 k = *reinterpret_cast<const float4*>(&KV[(kq + 16 * j) * kKPitch + c]);
-        acc0[j] += qv0[c] * k.x;
-        acc1[j] += qv1[c] * k.x;
-        acc0[j] += qv0[c + 1] * k.y;
-        acc1[j] += qv1[c + 1] * k.y;
-        acc0[j] += qv0[c + 2] * k.z;
-        acc1[j] += qv1[c + 2] * k.z;
-        acc0[j] += qv0[c + 3] * k.w;
-        acc1[j] += qv1[c + 3] * k.w;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      if (k0 + kq + 16 * j < L) {
-        S[qa * pitch + k0 + kq + 16 * j] = acc0[j] * kInvSqrtD;
-        S[(qa + 1) * pitch + k0 + kq + 16 * j] = acc1[j] * kInvSqrtD;
-      }
-    }
-  }
+  if (tid < kAttnQ)
+    s_max[tid] = fmaxf(fmaxf(s_maxw[0][tid], s_maxw[1][tid]), fmaxf(s_maxw[2][tid], s_maxw[3][tid]));
   __syncthreads();
 
-  // phases 2, 3 and 5 give one wave a whole row at a time: lane l covers the
-  // float4 columns 4l + 256i, so each LDS access is one contiguous run
-  const int wv = tid >> 6, ln = tid & 63;
-  // phase 2: row max (order-free) and phase 3: e_t = expf(s_t - max), 4 at a
-  // time (a row tail past L lies in the pitch padding and is never read back
-  // as a probability)
-  for (int q = wv; q < kAttnQ; q += 4) {
-    float* row = &S[q * pitch];
-    float m = -INFINITY;
-    for (int t = ln * 4; t < L; t += 256) {
-      const float4 v = *reinterpret_cast<const float4*>(row + t);
-      m = nanless_max(m, v.x);
-      if (t + 1 < L) m = nanless_max(m, v.y);
-      if (t + 2 < L) m = nanless_max(m, v.z);
-      if (t + 3 < L) m = nanless_max(m, v.w);
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
-    for (int t0 = 0; t0 < L; t0 += 256) {  // wave-uniform trip count (expf_libm needs all lanes)
-      const int t = t0 + ln * 4;
-      const bool in = t < L;
-      float4 v = in ? *reinterpret_cast<const float4*>(row + t) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // phase 3: e_t = expf(s_t - max) over the nq x ceil(L/4) float4s of the tile,
+  // spread over all lanes (entries past L are padding and never summed)
+  {
+    const int cols4 = (L + 3) >> 2;
+    const uint32_t magic = 0xffffffffu / (uint32_t)cols4 + 1u;  // u / cols4 = umulhi(u, magic) for u < 2^16
+    const int units = nq * cols4;
+    for (int u0 = 0; u0 < units; u0 += 256) {  // wave-uniform trip count (expf_libm needs all lanes)
+      const int u = min(u0 + tid, units - 1);
+      const int q = (int)__umulhi((uint32_t)u, magic);
+      const int c4 = u - q * cols4;
+      float* e = &S[q * pitch + 4 * c4];
+      float4 v = *reinterpret_cast<const float4*>(e);
+      const float m = s_max[q];
       v.x = expf_libm(v.x - m, tb);
       v.y = expf_libm(v.y - m, tb);
       v.z = expf_libm(v.z - m, tb);
       v.w = expf_libm(v.w - m, tb);
-      if (in) *reinterpret_cast<float4*>(row + t) = v;
+      if (u0 + tid < units) *reinterpret_cast<float4*>(e) = v;
     }
   }
   __syncthreads();
   // phase 4: in-order denominator, one lane per query
   if (tid < kAttnQ) {
-    const float* e = &S[tid * pitch];
-    float sum = 0.0f;
-    int t = 0;
-    for (; t + 4 <= L; t += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(e + t);
-      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    float inv = 0.0f;
+    if (tid < nq) {
+      const float* e = &S[tid * pitch];
+      float sum = 0.0f;
+      int t = 0;
+      for (; t + 4 <= L; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(e + t);
+        sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+      }
+      for (; t < L; t++) sum += e[t];
+      inv = 1.0f / sum;
     }
-    for (; t < L; t++) sum += e[t];
-    s_inv[tid] = 1.0f / sum;
-  }
-  __syncthreads();
-  // phase 5: p_t = e_t * inv
-  for (int q = wv; q < kAttnQ; q += 4) {
-    float* row = &S[q * pitch];
-    const float inv = s_inv[q];
-    for (int t = ln * 4; t < L; t += 256) {
-      float4 v = *reinterpret_cast<const float4*>(row + t);
-      v.x = v.x * inv; v.y = v.y * inv; v.z = v.z * inv; v.w = v.w * inv;
-      *reinterpret_cast<float4*>(row + t) = v;
-    }
+    s_inv[tid] = inv;
   }
 
-  // phase 6: ctx_d = sum_t p_t * v_t,d in order. thread -> d (tid % 32) x 4 queries
-  const int d = tid & 31, pg = tid >> 5;
+  // phase 6: ctx[q][d] = sum_t p_t * v_t,d in order, p_t = e_t * inv.  Wave w
+  // owns the 16 x 16 quadrant (query half w/2, dim half w%2); one MFMA covers
+  // 4 consecutive keys: A = P (query x key), B = V (key x dim).  Lane l ends with
+  // queries 16qh + 4lg + i at dim 16dh + lr.  V fragments come from global
+  // memory 16 keys ahead, into ping-pong registers.
+  __syncthreads();  // publishes s_inv
+  const int qh = wave >> 1, dh = wave & 1;
+  const bool has_item = qh < nqh;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k0 = 0; k0 < L; k0 += kKeyChunk) {
-    __syncthreads();
+  if (has_item) {
+    const float* prow = &S[(16 * qh + lr) * pitch + lg];
+    const float inv = s_inv[16 * qh + lr];
+    const int voff = lg * HQKV + 2 * H + 16 * dh + lr;  // lane part of the V fragment address
+    // full groups of 16 keys: no masking; group starts of the prefetch are
+    // clamped to the last full group (wave-uniform)
+    const int Lf = L & ~15;
+    auto load_v = [&](int t0, float (&v)[4]) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int idx = tid + i * 256, key = idx >> 3, c4 = idx & 7;
-      const int kr = min(k0 + key, L - 1);
-      *reinterpret_cast<float4*>(&KV[key * kKPitch + c4 * 4]) =
-          *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + kr) * HQKV + 2 * H + h * 32 + c4 * 4);
+      for (int u = 0; u < 4; u++) v[u] = (qkv + (size_t)(t0 + 4 * u) * HQKV)[voff];
+    };
+    auto pv_group = [&](int t0, const float (&v)[4]) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[t0 + 4 * u] * inv, v[u]));
+    };
+    // 4-deep register ring: each group's V is requested 48 keys ahead
+    float v0[4], v1[4], v2[4], v3[4];
+    if (Lf > 0) {
+      load_v(0, v0);
+      load_v(min(16, Lf - 16), v1);
+      load_v(min(32, Lf - 16), v2);
     }
-    __syncthreads();
-    const int nk = min(kKeyChunk, L - k0);
-    int t = 0;
-    for (; t + 4 <= nk; t += 4) {
-      const float v0 = KV[t * kKPitch + d], v1 = KV[(t + 1) * kKPitch + d];
-      const float v2 = KV[(t + 2) * kKPitch + d], v3 = KV[(t + 3) * kKPitch + d];
+    for (int t0 = 0; t0 < Lf; t0 += 64) {
+      load_v(min(t0 + 48, Lf - 16), v3);
+      pv_group(t0, v0);
+      if (t0 + 16 >= Lf) break;
+      load_v(min(t0 + 64, Lf - 16), v0);
+      pv_group(t0 + 16, v1);
+      if (t0 + 32 >= Lf) break;
+      load_v(min(t0 + 80, Lf - 16), v1);
+      pv_group(t0 + 32, v2);
+      if (t0 + 48 >= Lf) break;
+      load_v(min(t0 + 96, Lf - 16), v2);
+      pv_group(t0 + 48, v3);
+    }
+    // last L - Lf (< 16) keys: keys past the segment contribute exact zeros
+    for (int t0 = Lf; t0 < L; t0 += 4) {
+      const int t = t0 + lg;
+      const bool in = t < L;
+      const float e = prow[min(t, L - 1) - lg];
+      const float v = (qkv + (size_t)min(t, L - 1) * HQKV)[voff - lg * HQKV];
+      add_blocks(acc, mfma_products(in ? e * inv : 0.0f, in ? v : 0.0f));
+    }
+  }
+  if (has_item) {
+    const int d = 16 * dh + lr;
+    const float sm = p.rowmax ? p.smooth[h * 32 + d] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 pp = *reinterpret_cast<const float4*>(&S[(pg * 4 + j) * pitch + k0 + t]);
-        acc[j] = acc[j] + pp.x * v0;
-        acc[j] = acc[j] + pp.y * v1;
-        acc[j] = acc[j] + pp.z * v2;
-        acc[j] = acc[j] + pp.w * v3;
+    for (int i = 0; i < 4; i++) {
+      const int q = 16 * qh + 4 * lg + i;
+      if (q < nq) p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = acc[i];
+      if (p.rowmax) {
+        float a = nanless_max(0.0f, fabsf(acc[i] * sm));
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
+        if (q < nq && lr == 0) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
       }
     }
-    for (; t < nk; t++) {
-      const float v = KV[t * kKPitch + d];
-#pragma unroll
-      for (int j = 0; j < 4; j++) acc[j] = acc[j] + S[(pg * 4 + j) * pitch + k0 + t] * v;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int q = pg * 4 + j;
-    const float o = acc[j];
-    if (q < nq) p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = o;
-    if (p.rowmax) {
-      float a = q < nq ? fabsf(o * p.smooth[h * 32 + d]) : 0.0f;
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
-      if (q < nq && d == 0) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
-    }
   }
 }
 
-size_t attention_lds_bytes(int s_pitch) {
-  return sizeof(float) * ((size_t)kAttnQ * s_pitch + kKeyChunk * kKPitch + kAttnQ * 32);
-}
+size_t attention_lds_bytes(int s_pitch) { return sizeof(float) * (size_t)kAttnQ * s_pitch; }
 
 int attention_pitch(int max_len) {
   const int L = max(1, min(max_len, 512));
-  return ((L + 3) / 4) * 4 + 4;
+  return ((L + 15) / 16) * 16 + 4;
 }
 
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
@@ -253,9 +436,10 @@ void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_lds_bytes(attention_pitch(512)));
     lds_raised = true;
   }
-  hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.tile_start);
-  if (max_tiles > 0)
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
+  if (p.s_pitch - 4 > kAttnShortMax && max_tiles > 0)
     hipLaunchKernelGGL(attention_kernel, dim3(max_tiles, 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p);
+  hipLaunchKernelGGL(attention_short_kernel, dim3(p.B, 12), dim3(64), 0, st, p);
 }
 
 // ---------------------------------------------------------------------------

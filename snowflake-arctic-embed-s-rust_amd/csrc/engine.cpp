@@ -141,7 +141,7 @@ struct ae_workspace {
   int max_tokens = 0, max_seqs = 0;
   uint16_t* ids = nullptr;
   int* cu = nullptr;
-  int* tile_start = nullptr;
+  int* attn_plan = nullptr;  // attention work plan, attention_plan_ints(max_seqs)
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
@@ -333,7 +333,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
-      AttnArgs a{ws->qkv, cu, B, ws->tile_start, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
+      AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
       launch_attention(a, max_tiles, st);
     }
     {
@@ -527,7 +527,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
     return rc;
   };
   int rc;
-  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->tile_start, B + 1)) ||
+  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->attn_plan, aek::attention_plan_ints(int(B)))) ||
       (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
       (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
       (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
@@ -700,13 +700,13 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   if (!qkv_dev || !cu_seqlens_dev || !ctx_dev || n_seqs < 0 || total_tokens < 0)
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
   if (n_seqs == 0) return AE_OK;
-  int* tile_start = nullptr;
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&tile_start), size_t(n_seqs + 1) * sizeof(int)));
-  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, tile_start, ctx_dev, nullptr, nullptr,
+  int* plan = nullptr;
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs) * sizeof(int)));
+  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
                   aek::attention_pitch(ae::kMaxPos)};
   aek::launch_attention(a, total_tokens / 32 + n_seqs + 1, as_stream(stream));
   hipError_t err = hipStreamSynchronize(as_stream(stream));
-  (void)hipFree(tile_start);
+  (void)hipFree(plan);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));
   return AE_OK;
 }

@@ -67,7 +67,7 @@ struct AttnArgs {
   const float* qkv;        // [T,1152]
   const int* cu;           // [B+1]
   int B;
-  int* tile_start;         // [B+1] scratch
+  int* plan;               // [2B+2] scratch: long-tile prefix [B+1], then short count + short list [B+1]
   float* ctx;              // [T,384]
   const float* smooth;     // attn_out inv_smooth [384] or null
   uint32_t* rowmax;        // [T] or null
@@ -75,7 +75,11 @@ struct AttnArgs {
 };
 int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
-// tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32)
+// ints of `plan` scratch needed for B segments
+inline size_t attention_plan_ints(int B) { return 2 * (size_t)B + 2; }
+// segments of length <= kAttnShortMax run one wave per (segment, head); longer
+// ones in tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32)
+constexpr int kAttnShortMax = 64;
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st);
 
 struct ClsArgs {
