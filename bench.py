@@ -96,6 +96,19 @@ def gemm_microbench(ae, torch, iters):
     return rows
 
 
+def measured_traffic(kind, workload):
+    """HBM bytes per launch of `kind` on `workload`, from a committed rocprofv3 --pmc summary
+    (profiles/<kind>_<workload>_traffic.txt, line `hbm_bytes_per_launch: N`), or None."""
+    path = os.path.join(ROOT, "profiles", "%s_%s_traffic.txt" % (kind, workload))
+    try:
+        for ln in open(path):
+            if ln.startswith("hbm_bytes_per_launch:"):
+                return int(float(ln.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
+
+
 def load_cpu_oracle():
     """The oracle (scalar restatement of the reference), used only by the cpu_baseline leg."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -113,6 +126,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c1", action="store_true", help="skip the 128-token latency measurement")
     ap.add_argument("--gemm", action="store_true", help="run only the configs[1] GEMM microbench")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on exactly one GPU (the forward pass is data-parallel over sequences "
@@ -149,6 +164,13 @@ def main():
         engine.forward_packed_device(ws, ids_d.data_ptr(), cu_d.data_ptr(), B, T, out_d.data_ptr(), ws.stream,
                                      max_seq_len=max(lens))
 
+    if args.calib_copy_mib > 0:  # one copy kernel of known size: reads N MiB, writes N MiB
+        src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -178,7 +200,7 @@ def main():
     avg_launch_s = ktimes[dom][0] / 1e3 / max(1, launches)
     achieved = amount / avg_launch_s / (1e9 if unit == "GB/s" else 1e12)
     roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 3), "peak": peak,
-                "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+                "unit": unit, "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom, workload),
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "algorithmic_per_launch": amount}
     # the FFN GEMMs' fraction of dense int8 MFMA peak (BASELINE metric, part 2)
     ffn = {}
@@ -228,11 +250,13 @@ def main():
         cpu_s = time.perf_counter() - t0
         m.close()
         g = emb[: len(sample)].astype(np.float64)
-        cos = float(((g * ref).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(ref, axis=1))).min())
+        r = np.asarray(ref, np.float64)
+        cos = float(((g * r).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(r, axis=1))).min())
+        same = bool(np.array_equal(emb[: len(sample)].view(np.uint32), np.asarray(ref, np.float32).view(np.uint32)))
         cpu = {"value": round(len(sample) / cpu_s, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
                "sample": "first %d sequences (%d tokens) of the %s batch, scalar oracle, embed_batch policy"
                          % (len(sample), sum(len(s) for s in sample), workload),
-               "gpu_vs_cpu_min_cos": round(cos, 9)}
+               "gpu_vs_cpu_min_cos": round(cos, 12), "gpu_vs_cpu_bit_identical": same}
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1, "steps": args.steps,

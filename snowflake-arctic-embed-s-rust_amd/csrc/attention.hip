@@ -17,176 +17,44 @@ namespace aek {
 //   ctx_d = sum_{t in order} p_t * v_t,d
 // every sum left to right with separately rounded products.
 //
-// Segments longer than kAttnShortMax: a WG (tile, head) owns kAttnQ queries of
-// one sequence.  Scores for all keys of the sequence stay in LDS (row pitch =
-// padded max length); the score, exp and PV phases use all 256 lanes, only the
-// in-order softmax denominator is one lane per query.  Shorter segments go to
-// attention_short_kernel (one wave per segment and head).  Both fold the
-// SmoothQuant row absmax of the output (|ctx_j * inv_smooth_j|) into `rowmax`
-// (atomicMax on non-negative f32 bits), which the attn_out GEMM prologue
-// consumes.
+// A workgroup (tile, head) owns kAttnQ queries of one sequence.  Scores for all
+// keys of the sequence stay in LDS (row pitch = padded max length); the score,
+// exp and PV phases use all 256 lanes, only the in-order softmax denominator is
+// one lane per query.  The kernel also folds the SmoothQuant row absmax of its
+// output (|ctx_j * inv_smooth_j|) into `rowmax` (atomicMax on non-negative f32
+// bits), which the attn_out GEMM prologue consumes.
 // ---------------------------------------------------------------------------
 constexpr int kAttnQ = 32;     // queries per workgroup
 
-// Work plan, built on the device from cu_seqlens: segments of 1..kAttnShortMax
-// tokens go to the short kernel (plan[B+1] = their count, plan[B+2..] = their
-// indices in order); longer ones to the tiled kernel, which finds its segment
-// from plan[b] = sum_{b'<b} long tiles of b' (plan[B] = total).
-__device__ __forceinline__ int long_tiles(int L) { return L > kAttnShortMax ? (L + kAttnQ - 1) / kAttnQ : 0; }
-__device__ __forceinline__ int is_short(int L) { return L >= 1 && L <= kAttnShortMax ? 1 : 0; }
-
+// Work plan, built on the device from cu_seqlens: plan[b] = sum_{b'<b}
+// ceil(L_b'/kAttnQ) (plan[B] = number of tiles) and, after it, tile_seg[tile] =
+// the segment of each tile, so a workgroup finds its segment with one load.
 __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int* plan) {
-  __shared__ int part_t[256], part_s[256];
+  __shared__ int part[256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
-  int nt = 0, ns = 0;
-  for (int b = b0; b < b1; b++) {
-    const int L = cu[b + 1] - cu[b];
-    nt += long_tiles(L);
-    ns += is_short(L);
-  }
-  part_t[tid] = nt;
-  part_s[tid] = ns;
+  int nt = 0;
+  for (int b = b0; b < b1; b++) nt += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
+  part[tid] = nt;
   __syncthreads();
   if (tid == 0) {
-    int at = 0, as = 0;
+    int acc = 0;
     for (int i = 0; i < 256; i++) {
-      const int vt = part_t[i], vs = part_s[i];
-      part_t[i] = at;
-      part_s[i] = as;
-      at += vt;
-      as += vs;
+      const int v = part[i];
+      part[i] = acc;
+      acc += v;
     }
-    plan[B] = at;
-    plan[B + 1] = as;
+    plan[B] = acc;
   }
   __syncthreads();
-  int at = part_t[tid], as = part_s[tid];
-  int* short_list = plan + B + 2;
+  int* tile_seg = plan + B + 1;
+  int at = part[tid];
   for (int b = b0; b < b1; b++) {
-    const int L = cu[b + 1] - cu[b];
     plan[b] = at;
-    at += long_tiles(L);
-    if (is_short(L)) short_list[as++] = b;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Short segments (1..64 tokens): one wave per (segment, head), lane = query.
-// Each lane runs the reference's scalar sequence for its own query row
-// (scores, max, exp with the in-order sum, normalise, in-order PV) over its own
-// LDS row, so no barrier is needed.  The K and V rows are the same for every
-// lane: they are read once per wave through the scalar data cache (constant
-// address space, uniform addresses) into two ping-pong register sets, one key
-// ahead of their use, and enter the VALU as scalar operands.
-// ---------------------------------------------------------------------------
-constexpr int kShortPitch = kAttnShortMax + 4;  // LDS floats per lane row (16-byte aligned rows)
-
-typedef const float __attribute__((address_space(4)))* uniform_fptr;
-
-__device__ __forceinline__ uniform_fptr as_uniform(const float* p) { return (uniform_fptr)(uintptr_t)p; }
-
-__device__ __forceinline__ void load_row32(uniform_fptr r, float (&x)[32]) {
-#pragma unroll
-  for (int i = 0; i < 32; i++) x[i] = r[i];
-}
-
-// dot32_f32 scalar order (src/simd_math.rs:1461-1468), times 1/sqrt(32)
-__device__ __forceinline__ float score32(const float (&q)[32], const float (&k)[32]) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i++) acc += q[i] * k[i];
-  return acc * kInvSqrtD;
-}
-
-__device__ __forceinline__ void pv_step(float (&o)[32], float pt, const float (&v)[32]) {
-#pragma unroll
-  for (int d = 0; d < 32; d++) o[d] = o[d] + pt * v[d];
-}
-
-__global__ __launch_bounds__(64) void attention_short_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) float S[64 * kShortPitch];
-  const int* short_list = p.plan + p.B + 1;  // [0] = count
-  const int item = blockIdx.x, h = blockIdx.y;
-  if (item >= short_list[0]) return;
-  const int b = short_list[1 + item];
-  const int s0 = p.cu[b];
-  const int L = p.cu[b + 1] - s0;  // 1..kAttnShortMax (the plan guarantees it)
-  const int lane = threadIdx.x;
-  const ExpTab tb = exp_tab_regs();
-  float* row = S + lane * kShortPitch;
-  const int qi = min(lane, L - 1);  // lanes past the segment repeat its last query; never stored
-  float q[32];
-#pragma unroll
-  for (int c = 0; c < 32; c += 4) {
-    const float4 v = *reinterpret_cast<const float4*>(p.qkv + (size_t)(s0 + qi) * HQKV + h * 32 + c);
-    q[c] = v.x; q[c + 1] = v.y; q[c + 2] = v.z; q[c + 3] = v.w;
-  }
-  const uniform_fptr kbase = as_uniform(p.qkv + (size_t)s0 * HQKV + H + h * 32);
-  const uniform_fptr vbase = as_uniform(p.qkv + (size_t)s0 * HQKV + 2 * H + h * 32);
-  const int last = L - 1;
-
-  // scores and row max; keys in pairs (A, B), the prefetched row clamped to the segment
-  float ka[32], kb[32];
-  float m = -INFINITY;
-  load_row32(kbase, ka);
-  int t = 0;
-  for (; t + 1 < L; t += 2) {
-    load_row32(kbase + (t + 1) * HQKV, kb);
-    const float sa = score32(q, ka);
-    load_row32(kbase + min(t + 2, last) * HQKV, ka);
-    const float sb = score32(q, kb);
-    row[t] = sa;
-    row[t + 1] = sb;
-    m = nanless_max(nanless_max(m, sa), sb);
-  }
-  if (t < L) {  // odd length: key L-1 is in ka
-    const float sa = score32(q, ka);
-    row[t] = sa;
-    m = nanless_max(m, sa);
-  }
-  // e_t = expf(s_t - max) with the in-order sum, 4 keys per LDS access (entries
-  // past L are pitch padding: their exps are discarded and add nothing)
-  float sum = 0.0f;
-  for (int t4 = 0; t4 < L; t4 += 4) {
-    float4 v = *reinterpret_cast<const float4*>(row + t4);
-    v.x = expf_libm(v.x - m, tb);
-    v.y = expf_libm(v.y - m, tb);
-    v.z = expf_libm(v.z - m, tb);
-    v.w = expf_libm(v.w - m, tb);
-    *reinterpret_cast<float4*>(row + t4) = v;
-    sum += v.x;
-    if (t4 + 1 < L) sum += v.y;
-    if (t4 + 2 < L) sum += v.z;
-    if (t4 + 3 < L) sum += v.w;
-  }
-  const float inv = 1.0f / sum;
-  // ctx_d = sum_t (e_t * inv) * v_t,d in order
-  float o[32];
-#pragma unroll
-  for (int d = 0; d < 32; d++) o[d] = 0.0f;
-  load_row32(vbase, ka);
-  t = 0;
-  for (; t + 1 < L; t += 2) {
-    load_row32(vbase + (t + 1) * HQKV, kb);
-    const float2 e2 = *reinterpret_cast<const float2*>(row + t);
-    pv_step(o, e2.x * inv, ka);
-    load_row32(vbase + min(t + 2, last) * HQKV, ka);
-    pv_step(o, e2.y * inv, kb);
-  }
-  if (t < L) pv_step(o, row[t] * inv, ka);
-
-  if (lane < L) {
-    float* dst = p.ctx + (size_t)(s0 + lane) * H + h * 32;
-#pragma unroll
-    for (int d = 0; d < 32; d += 4) *reinterpret_cast<float4*>(dst + d) = make_float4(o[d], o[d + 1], o[d + 2], o[d + 3]);
-    if (p.rowmax) {
-      float a = 0.0f;
-#pragma unroll
-      for (int d = 0; d < 32; d++) a = nanless_max(a, fabsf(o[d] * p.smooth[h * 32 + d]));
-      atomicMax(&p.rowmax[s0 + lane], __float_as_uint(a));
-    }
+    const int n = (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
+    for (int i = 0; i < n; i++) tile_seg[at + i] = b;
+    at += n;
   }
 }
 
@@ -216,19 +84,25 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 }
 
 // dynamic LDS: S[kAttnQ][s_pitch] scores -> exps, s_pitch = round16(max length) + 4
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
+// Workgroups are dispatched round-robin over the 8 XCDs (WG p -> XCD p % 8),
+// each with its own L2.  Renumber them so that XCD x runs one contiguous range
+// of logical work items: the tiles of one (sequence, head), which share that
+// head's K and V, then run on one XCD and hit in its L2.
+__device__ __forceinline__ int xcd_contiguous(int p, int n) {
+  const int q = n >> 3, r = n & 7, x = p & 7, i = p >> 3;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
+// grid: max_tiles * 12 workgroups; logical item = head * max_tiles + tile
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kAttnQ];
   __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
-  const int tile = blockIdx.x, h = blockIdx.y;
+  const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
+  const int h = item / max_tiles, tile = item - h * max_tiles;
   const int* tile_start = p.plan;
   if (tile >= tile_start[p.B]) return;
-  int lo = 0, hi = p.B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
-  }
-  const int b = lo;
+  const int b = tile_start[p.B + 1 + tile];  // tile_seg
   const int s0 = p.cu[b];
   const int pitch = p.s_pitch;
   const int L = min(p.cu[b + 1] - s0, pitch - 4);  // the host sizes pitch >= round16(L) + 4
@@ -318,11 +192,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
   // spread over all lanes (entries past L are padding and never summed)
   {
     const int cols4 = (L + 3) >> 2;
-    const uint32_t magic = 0xffffffffu / (uint32_t)cols4 + 1u;  // u / cols4 = umulhi(u, magic) for u < 2^16
+    // q = u / cols4 as floor((u + 0.5) * (1/cols4)) in f32: exact for u < 2^13 and
+    // cols4 <= 128 (the quotient stays >= 0.5/cols4 away from an integer, far
+    // above the rounding error)
+    const float rcols = 1.0f / (float)cols4;
     const int units = nq * cols4;
     for (int u0 = 0; u0 < units; u0 += 256) {  // wave-uniform trip count (expf_libm needs all lanes)
       const int u = min(u0 + tid, units - 1);
-      const int q = (int)__umulhi((uint32_t)u, magic);
+      const int q = (int)(((float)u + 0.5f) * rcols);
       const int c4 = u - q * cols4;
       float* e = &S[q * pitch + 4 * c4];
       float4 v = *reinterpret_cast<const float4*>(e);
@@ -437,9 +314,9 @@ void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
     lds_raised = true;
   }
   hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
-  if (p.s_pitch - 4 > kAttnShortMax && max_tiles > 0)
-    hipLaunchKernelGGL(attention_kernel, dim3(max_tiles, 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p);
-  hipLaunchKernelGGL(attention_short_kernel, dim3(p.B, 12), dim3(64), 0, st, p);
+  if (max_tiles > 0)
+    hipLaunchKernelGGL(attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p,
+                       max_tiles);
 }
 
 // ---------------------------------------------------------------------------

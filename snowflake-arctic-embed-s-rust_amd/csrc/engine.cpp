@@ -141,7 +141,7 @@ struct ae_workspace {
   int max_tokens = 0, max_seqs = 0;
   uint16_t* ids = nullptr;
   int* cu = nullptr;
-  int* attn_plan = nullptr;  // attention work plan, attention_plan_ints(max_seqs)
+  int* attn_plan = nullptr;  // attention work plan, attention_plan_ints(max_seqs, max_tokens)
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
@@ -322,7 +322,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.rowmax_init = ws->rowmax_ctx;
     launch_ln_quant(p, kLnSrcEmb, st);
   }
-  const int max_tiles = T / 32 + B + 1;  // >= sum_b ceil(L_b / 32)
+  const int max_tiles = attention_max_tiles(B, T);
   const int s_pitch = attention_pitch(max_len);
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
@@ -527,7 +527,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
     return rc;
   };
   int rc;
-  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->attn_plan, aek::attention_plan_ints(int(B)))) ||
+  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->attn_plan, aek::attention_plan_ints(int(B), int(T)))) ||
       (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
       (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
       (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
@@ -701,10 +701,10 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
   if (n_seqs == 0) return AE_OK;
   int* plan = nullptr;
-  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs) * sizeof(int)));
+  HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs, total_tokens) * sizeof(int)));
   aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
                   aek::attention_pitch(ae::kMaxPos)};
-  aek::launch_attention(a, total_tokens / 32 + n_seqs + 1, as_stream(stream));
+  aek::launch_attention(a, aek::attention_max_tiles(n_seqs, total_tokens), as_stream(stream));
   hipError_t err = hipStreamSynchronize(as_stream(stream));
   (void)hipFree(plan);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));

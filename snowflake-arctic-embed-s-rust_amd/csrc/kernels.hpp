@@ -67,7 +67,7 @@ struct AttnArgs {
   const float* qkv;        // [T,1152]
   const int* cu;           // [B+1]
   int B;
-  int* plan;               // [2B+2] scratch: long-tile prefix [B+1], then short count + short list [B+1]
+  int* plan;               // scratch: attention_plan_ints(B, T) ints
   float* ctx;              // [T,384]
   const float* smooth;     // attn_out inv_smooth [384] or null
   uint32_t* rowmax;        // [T] or null
@@ -75,11 +75,10 @@ struct AttnArgs {
 };
 int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
-// ints of `plan` scratch needed for B segments
-inline size_t attention_plan_ints(int B) { return 2 * (size_t)B + 2; }
-// segments of length <= kAttnShortMax run one wave per (segment, head); longer
-// ones in tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32)
-constexpr int kAttnShortMax = 64;
+// tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32); T/32 + B + 1 is one
+inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
+// ints of `plan` scratch for B segments and T tokens: tile prefix [B+1] + tile_seg [max_tiles]
+inline size_t attention_plan_ints(int B, int T) { return (size_t)B + 1 + attention_max_tiles(B, T); }
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st);
 
 struct ClsArgs {
