@@ -122,7 +122,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-sample", type=int, default=32, help="sequences of the workload timed on the CPU")
+    ap.add_argument("--cpu-sample", type=int, default=256, help="sequences of the workload timed on the CPU")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c1", action="store_true", help="skip the 128-token latency measurement")
     ap.add_argument("--gemm", action="store_true", help="run only the configs[1] GEMM microbench")

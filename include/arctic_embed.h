@@ -195,6 +195,11 @@ int ae_debug_forward_prefix(const ae_engine* e, ae_workspace* ws, const uint16_t
                             size_t n, int layers, float* hidden, int8_t* act_q, float* act_scale);
 /* Device GELU (the reference's scalar_gelu, src/simd_math.rs:15-23) over n floats. */
 int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream);
+/* The attention kernels' multiplier: v_mfma_f32_16x16x1_4b_f32 with a zero
+ * accumulator over n_sets sets of 64 operand pairs (a_dev, b_dev: n_sets*64
+ * floats).  out_dev[(set*64 + lane)*16 + r] = a[set*64 + blk*16 + m] *
+ * b[set*64 + blk*16 + n] with blk = r/4, m = 4*(lane/16) + r%4, n = lane%16. */
+int ae_debug_mfma_products(const float* a_dev, const float* b_dev, float* out_dev, int n_sets, void* stream);
 
 #ifdef __cplusplus
 }

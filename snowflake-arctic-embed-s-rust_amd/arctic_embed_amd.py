@@ -71,6 +71,7 @@ _SIGS = {
     "ae_tokenizer_encode": (_i32, [_vp, _c.c_char_p, _i32, _vp, _sz, _c.POINTER(_sz)]),
     "ae_tokenizer_vocab_size": (_sz, [_vp]),
     "ae_debug_gelu_map": (_i32, [_vp, _vp, _sz, _vp]),
+    "ae_debug_mfma_products": (_i32, [_vp, _vp, _vp, ctypes.c_int, _vp]),
     "ae_workspace_set_timing": (_i32, [_vp, _i32]),
     "ae_debug_forward_prefix": (_i32, [_vp, _vp, _vp, _vp, _sz, _i32, _vp, _vp, _vp]),
     "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
@@ -360,3 +361,8 @@ def attention_varlen(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None
 
 def gelu_map(x_ptr, y_ptr, n, stream=None):
     _check(_lib.ae_debug_gelu_map(x_ptr, y_ptr, int(n), stream))
+
+
+def mfma_products(a_ptr, b_ptr, out_ptr, n_sets, stream=None):
+    """Raw results of the attention kernels' exact-product MFMA (16 floats per lane per set of 64 pairs)."""
+    _check(_lib.ae_debug_mfma_products(a_ptr, b_ptr, out_ptr, int(n_sets), stream))

@@ -299,6 +299,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   }
 }
 
+// test hook: for each set of 64 operand pairs, the 16 results per lane of
+// mfma_products (out[set][lane][r]), the multiplier attention_kernel relies on
+__global__ __launch_bounds__(64) void mfma_products_kernel(const float* a, const float* b, float* out, int n_sets) {
+  const int set = blockIdx.x, l = threadIdx.x;
+  const v16f d = mfma_products(a[set * 64 + l], b[set * 64 + l]);
+#pragma unroll
+  for (int r = 0; r < 16; r++) out[((size_t)set * 64 + l) * 16 + r] = d[r];
+}
+void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st) {
+  if (n_sets > 0) hipLaunchKernelGGL(mfma_products_kernel, dim3(n_sets), dim3(64), 0, st, a, b, out, n_sets);
+}
+
 size_t attention_lds_bytes(int s_pitch) { return sizeof(float) * (size_t)kAttnQ * s_pitch; }
 
 int attention_pitch(int max_len) {

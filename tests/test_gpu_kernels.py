@@ -197,3 +197,52 @@ def test_attention_bit_exact(torch_gpu):
     torch.cuda.synchronize()
     ref = orc.attention(qkv, cu)
     assert np.array_equal(bits(ctx_d.cpu().numpy()), bits(ref))
+
+
+def test_mfma_products_equal_rounded_products(torch_gpu):
+    """The attention kernels take every product from v_mfma_f32_16x16x1_4b_f32 with a zero
+    accumulator: each result must be the correctly rounded f32 product (numpy's), including
+    denormal results, infinities and NaN; only the sign of an exact zero may differ."""
+    torch = torch_gpu
+    rng = np.random.default_rng(17)
+    n_sets = 2048
+    a = np.ldexp(rng.uniform(-1, 1, (n_sets, 64)), rng.integers(-80, 66, (n_sets, 64))).astype(f32)
+    b = np.ldexp(rng.uniform(-1, 1, (n_sets, 64)), rng.integers(-80, 66, (n_sets, 64))).astype(f32)
+    a[:64] = np.ldexp(rng.uniform(-1, 1, (64, 64)), -70).astype(f32)  # denormal products
+    b[:64] = np.ldexp(rng.uniform(-1, 1, (64, 64)), -75).astype(f32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38], f32)
+    a[64] = np.tile(special, 8)
+    b[64] = np.repeat(special, 8)
+    a_d, b_d = dev(torch, a), dev(torch, b)
+    out_d = torch.empty((n_sets, 64, 16), dtype=torch.float32, device="cuda")
+    ae.mfma_products(a_d.data_ptr(), b_d.data_ptr(), out_d.data_ptr(), n_sets)
+    torch.cuda.synchronize()
+    got = out_d.cpu().numpy()
+    lane = np.arange(64)[:, None]
+    r = np.arange(16)[None, :]
+    blk, m, n = r // 4, 4 * (lane // 16) + r % 4, lane % 16
+    with np.errstate(all="ignore"):
+        ref = a[:, blk * 16 + m] * b[:, blk * 16 + n]
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    same = (bits(got) == bits(ref)) | ((got == 0) & (ref == 0))
+    assert same[~nan].all()
+    assert np.count_nonzero((ref != 0) & (np.abs(ref) < np.finfo(f32).tiny)) > 1000  # denormals were covered
+
+
+def test_attention_bit_exact_extreme_magnitudes(torch_gpu):
+    """Scores and PV terms with denormal products, exact zeros and huge dynamic range."""
+    torch = torch_gpu
+    lens = [5, 40, 97, 300]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    rng = np.random.default_rng(23)
+    qkv = np.ldexp(rng.uniform(-1, 1, (T, 1152)), rng.integers(-70, 4, (T, 1152))).astype(f32)
+    qkv[::7, :] = 0.0
+    qkv[3::11, 384:768] *= -0.0
+    qkv_d, cu_d = dev(torch, qkv), dev(torch, cu)
+    ctx_d = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+    ae.attention_varlen(qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, ctx_d.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.attention(qkv, cu)
+    assert np.array_equal(bits(ctx_d.cpu().numpy()), bits(ref))
