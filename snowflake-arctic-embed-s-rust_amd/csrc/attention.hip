@@ -84,15 +84,8 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 }
 
 // dynamic LDS: S[kAttnQ][s_pitch] scores -> exps, s_pitch = round16(max length) + 4
-// Workgroups are dispatched round-robin over the 8 XCDs (WG p -> XCD p % 8),
-// each with its own L2.  Renumber them so that XCD x runs one contiguous range
-// of logical work items: the tiles of one (sequence, head), which share that
-// head's K and V, then run on one XCD and hit in its L2.
-__device__ __forceinline__ int xcd_contiguous(int p, int n) {
-  const int q = n >> 3, r = n & 7, x = p & 7, i = p >> 3;
-  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
-}
-
+// The tiles of one (sequence, head) share that head's K and V: with the
+// XCD-contiguous numbering (xcd_contiguous) they run on one XCD and hit in its L2.
 // grid: max_tiles * 12 workgroups; logical item = head * max_tiles + tile
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -219,6 +212,15 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
       const float* e = &S[tid * pitch];
       float sum = 0.0f;
       int t = 0;
+      for (; t + 32 <= L; t += 32) {  // 8 loads in flight per batch of 32 sequential adds
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = *reinterpret_cast<const float4*>(e + t + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          sum += v[i].x; sum += v[i].y; sum += v[i].z; sum += v[i].w;
+        }
+      }
       for (; t + 4 <= L; t += 4) {
         const float4 v = *reinterpret_cast<const float4*>(e + t);
         sum += v.x; sum += v.y; sum += v.z; sum += v.w;

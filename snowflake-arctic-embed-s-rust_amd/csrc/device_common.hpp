@@ -115,6 +115,15 @@ __device__ __forceinline__ float gelu_exact(float x, const ExpTab& tb) {
   return 0.5f * x * (1.0f + erf_val);
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (WG p -> XCD p % 8),
+// each with its own L2.  xcd_contiguous(p, n) renumbers the n workgroups of a
+// launch so that XCD x runs one contiguous range of logical items: neighbouring
+// items, which share input data, then run on one XCD and hit in its L2.
+__device__ __forceinline__ int xcd_contiguous(int p, int n) {
+  const int q = n >> 3, r = n & 7, x = p & 7, i = p >> 3;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+}
+
 // index of the segment containing token t: largest b with cu[b] <= t (cu has B+1 entries)
 __device__ __forceinline__ int find_segment(const int* cu, int B, int t) {
   int lo = 0, hi = B - 1;

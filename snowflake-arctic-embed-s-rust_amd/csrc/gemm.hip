@@ -32,9 +32,6 @@
 namespace aek {
 
 constexpr int kBM = 64;      // rows per workgroup
-constexpr int kBN = 384;     // columns per workgroup
-constexpr int kWaveN = 96;   // columns per wave
-constexpr int kCB = kWaveN / 16;
 constexpr int kAPitch = 80;  // LDS row pitch of the A tile (bytes): conflict-free fragment reads
 constexpr int kEPitch = 100; // LDS row pitch of the epilogue staging tile (words)
 
@@ -49,13 +46,42 @@ struct ARegs {
   float4 v[4];
 };
 
-template <int AM, int EM>
-__global__ __launch_bounds__(256, 2) void gemm_w8a8_kernel(GemmArgs p) {
+// Orders this wave's LDS accesses before and after it (LDS data private to one
+// wave needs no workgroup barrier: a wave's LDS operations complete in order once
+// the counter is drained).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// NW = columns per wave: 96 (workgroup = 384 columns, 2 waves/SIMD) or 48
+// (192 columns, 48 accumulator VGPRs: 4 waves/SIMD for int8 A, 3 for f32 A,
+// whose two-step register prefetch of A is four times larger).
+template <int AM, int EM, int NW>
+__global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm_w8a8_kernel(GemmArgs p) {
+  constexpr int kWaveN = NW, kBN = 4 * NW, kCB = NW / 16;
+  constexpr int kF4 = NW / 4;  // float4 columns of one wave row
   __shared__ __attribute__((aligned(16))) int8_t sA[2][kBM * kAPitch];
   __shared__ __attribute__((aligned(16))) int sE[4][16 * kEPitch];  // per-wave epilogue staging
   __shared__ uint32_t sRowMax[4][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;  // M tiles on x (y is limited to 65536)
+  // 1-D grid of (row tile, column tile) items.  f32 A (4 bytes per element):
+  // column tile fastest, numbered XCD-contiguously, so the column tiles of one
+  // row tile run back to back on one XCD and their A rows come from HBM once.
+  // int8 A: row tile fastest (neighbouring workgroups share W columns and do not
+  // contend on the same rows' GELU absmax atomics).
+  const int nt = p.N / kBN, mt = (p.M + kBM - 1) / kBM;
+  int m0, n0;
+  if constexpr (AM == kAI8) {
+    m0 = (blockIdx.x % mt) * kBM;
+    n0 = (blockIdx.x / mt) * kBN;
+  } else {
+    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    m0 = (item / nt) * kBM;
+    n0 = (item % nt) * kBN;
+  }
   const int KT = p.K >> 6;
   const int NB = p.N >> 4;  // 16-column fragments per K step in the swizzled W
   const ExpTab tb = exp_tab_regs();  // the epilogue loop below is wave-uniform
@@ -152,10 +178,10 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_kernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
     if (EM == kEpiGelu && lane < 16) sRowMax[wave][lane] = 0u;
-    __syncthreads();  // (wave-local data; also orders sRowMax resets)
+    wave_lds_sync();  // E and sRowMax are private to this wave
 #pragma unroll
-    for (int k = 0; k < 6; k++) {  // 16 rows x 24 float4 = 384 = 6 per lane
-      const int idx = lane + 64 * k, rr = idx / 24, c4 = idx % 24;
+    for (int k = 0; k < kF4 / 4; k++) {  // 16 rows x kF4 float4 over 64 lanes
+      const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
       const int row = m0 + i * 16 + rr;
       const bool ok = row < p.M;
       const int rrow = ok ? row : p.M - 1;
@@ -186,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_kernel(GemmArgs p) {
       }
       if (ok) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
     }
-    __syncthreads();
+    wave_lds_sync();
     if (EM == kEpiGelu && lane < 16) {
       const int row = m0 + i * 16 + lane;
       if (row < p.M) atomicMax(&p.g_rowmax[row], sRowMax[wave][lane]);
@@ -194,12 +220,18 @@ __global__ __launch_bounds__(256, 2) void gemm_w8a8_kernel(GemmArgs p) {
   }
 }
 
+// int8 A: 192-column workgroups (A is small and re-read once per column tile);
+// f32 A (quantized on load): 384-column workgroups, so each A row is read once.
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st) {
-  dim3 grid((p.M + kBM - 1) / kBM, p.N / kBN);
-  if (amode == kAI8 && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiF32>), grid, dim3(256), 0, st, p);
-  else if (amode == kAI8 && emode == kEpiGelu) hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiGelu>), grid, dim3(256), 0, st, p);
-  else if (amode == kAF32Q && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32Q, kEpiF32>), grid, dim3(256), 0, st, p);
-  else if (amode == kAF32QSmooth && emode == kEpiF32) hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32QSmooth, kEpiF32>), grid, dim3(256), 0, st, p);
+  const unsigned n = ((p.M + kBM - 1) / kBM) * (p.N / 192);  // 192-column workgroups
+  if (amode == kAI8 && emode == kEpiF32)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
+  else if (amode == kAI8 && emode == kEpiGelu)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiGelu, 48>), dim3(n), dim3(256), 0, st, p);
+  else if (amode == kAF32Q && emode == kEpiF32)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32Q, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
+  else if (amode == kAF32QSmooth && emode == kEpiF32)
+    hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32QSmooth, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
 }
 
 // [N,K] row-major int8 -> [K/64][N/16][64 lanes][16 bytes]: lane l of fragment
