@@ -177,6 +177,10 @@ int ae_write_synthetic_ae8(const char* path, uint64_t seed);
 #define AE_KERNEL_LAYER11_TAIL 8
 #define AE_KERNEL_KINDS 9
 int ae_workspace_set_timing(ae_workspace* ws, int enabled);
+/* Graph replay of repeated forward passes (on by default): the second call with
+ * the same buffers, stream and batch shape captures the pass into a hipGraph and
+ * later calls replay it.  Disabled while timing is on.  0 forces eager launches. */
+int ae_workspace_set_graphs(ae_workspace* ws, int enabled);
 int ae_workspace_kernel_times(ae_workspace* ws, double* ms_out, int* counts);
 /* The fused GEMM variants of the forward pass, exposed for parity tests:
  * A given as f32 rows quantized on load with q = round((x*s_k)*(127/rowmax[m]))

@@ -320,13 +320,14 @@ int attention_pitch(int max_len) {
   return ((L + 15) / 16) * 16 + 4;
 }
 
+// allow > 64 KiB of dynamic LDS for the tiled kernel on the current device; called
+// at engine open and by the stand-alone operator, never inside a stream capture
+void init_attention_kernels() {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)attention_lds_bytes(attention_pitch(512)));
+}
+
 void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
-  static bool lds_raised = false;  // once per process: allow > 64 KiB of dynamic LDS
-  if (!lds_raised) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_lds_bytes(attention_pitch(512)));
-    lds_raised = true;
-  }
   hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
   if (max_tiles > 0)
     hipLaunchKernelGGL(attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p,

@@ -161,8 +161,29 @@ struct ae_workspace {
   size_t ev_used = 0;
   double kind_ms[AE_KERNEL_KINDS] = {};
   int kind_count[AE_KERNEL_KINDS] = {};
+  // replay of captured forward passes (hipGraph), keyed by the launch parameters;
+  // a key is captured on its second use, so one-off batch shapes stay eager
+  struct GraphKey {
+    const void *ids, *cu, *out;
+    hipStream_t st;
+    int B, T, max_len;
+    bool operator==(const GraphKey& o) const {
+      return ids == o.ids && cu == o.cu && out == o.out && st == o.st && B == o.B && T == o.T && max_len == o.max_len;
+    }
+  };
+  struct GraphEntry {
+    GraphKey key;
+    hipGraphExec_t exec;  // null: seen once, not captured yet
+    uint64_t last_use;
+  };
+  bool graphs = true;
+  std::vector<GraphEntry> graph_cache;
+  uint64_t graph_tick = 0;
+  static constexpr size_t kGraphCacheSize = 8;
   ~ae_workspace() {
     if (stream) (void)hipStreamSynchronize(stream);
+    for (GraphEntry& g : graph_cache)
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
     for (hipEvent_t ev : ev_pool) (void)hipEventDestroy(ev);
     free_all(dev);
     if (h_ids) (void)hipHostFree(h_ids);
@@ -401,6 +422,55 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   return AE_OK;
 }
 
+// run_forward through the workspace's graph cache: the same launch parameters a
+// second time are captured into a hipGraph, later calls replay it (one launch
+// instead of ~90).  Eager when timing is on or the stream is already capturing.
+int run_forward_replay(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int T, int max_len, float* out,
+                       hipStream_t st) {
+  if (!ws->graphs || ws->timing) return run_forward(ws, ids, cu, B, T, max_len, out, st);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+    return run_forward(ws, ids, cu, B, T, max_len, out, st);
+  const ae_workspace::GraphKey key{ids, cu, out, st, B, T, max_len};
+  ws->graph_tick++;
+  ae_workspace::GraphEntry* hit = nullptr;
+  for (auto& g : ws->graph_cache)
+    if (g.key == key) hit = &g;
+  if (hit && hit->exec) {
+    hit->last_use = ws->graph_tick;
+    HIP_TRY(hipGraphLaunch(hit->exec, st));
+    return AE_OK;
+  }
+  if (!hit) {  // first use: remember the key, run eagerly
+    if (ws->graph_cache.size() >= ae_workspace::kGraphCacheSize) {
+      auto lru = std::min_element(ws->graph_cache.begin(), ws->graph_cache.end(),
+                                  [](const auto& a, const auto& b) { return a.last_use < b.last_use; });
+      if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+      ws->graph_cache.erase(lru);
+    }
+    ws->graph_cache.push_back({key, nullptr, ws->graph_tick});
+    return run_forward(ws, ids, cu, B, T, max_len, out, st);
+  }
+  // second use: capture, instantiate, launch
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  const int rc = run_forward(ws, ids, cu, B, T, max_len, out, st);
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(st, &graph);
+  if (rc != AE_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  if (end != hipSuccess || !graph) return fail(AE_ERR_HIP, std::string("graph capture: ") + hipGetErrorString(end));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (inst != hipSuccess) return fail(AE_ERR_HIP, std::string("graph instantiate: ") + hipGetErrorString(inst));
+  hit->exec = exec;
+  hit->last_use = ws->graph_tick;
+  HIP_TRY(hipGraphLaunch(exec, st));
+  return AE_OK;
+}
+
 // Runs `n` pre-tokenized sequences (already validated and truncated) through as
 // few device batches as the workspace capacity allows.  Sequences are length-
 // sorted so each batch packs similar lengths (length-bucketed packing); results
@@ -430,7 +500,7 @@ int run_sequences(const ae_engine* e, ae_workspace* ws, const std::vector<const 
     HIP_TRY(hipMemcpyAsync(ws->ids, ws->h_ids, size_t(T) * sizeof(uint16_t), hipMemcpyHostToDevice, ws->stream));
     HIP_TRY(hipMemcpyAsync(ws->cu, ws->h_cu, size_t(B + 1) * sizeof(int), hipMemcpyHostToDevice, ws->stream));
     const int max_len = lens[order[i + B - 1]];  // length-sorted: the last is the longest
-    if (int rc = run_forward(ws, ws->ids, ws->cu, B, T, max_len, ws->out_c, ws->stream)) return rc;
+    if (int rc = run_forward_replay(ws, ws->ids, ws->cu, B, T, max_len, ws->out_c, ws->stream)) return rc;
     HIP_TRY(hipMemcpyAsync(ws->h_out, ws->out_c, size_t(B) * ae::kHidden * sizeof(float), hipMemcpyDeviceToHost,
                            ws->stream));
     HIP_TRY(hipStreamSynchronize(ws->stream));
@@ -482,6 +552,7 @@ int ae_engine_open_files(const char* ae8_path, const char* vocab_path, ae_engine
   e->raw_size_bytes = m.size_bytes();
   if (int rc = check_device(&e->device)) return rc;
   if (int rc = upload_model(m, e.get())) return rc;
+  aek::init_attention_kernels();
   *out = e.release();
   return AE_OK;
 }
@@ -612,8 +683,8 @@ int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_
   if (n_seqs > ws->max_seqs || total_tokens > ws->max_tokens)
     return fail(AE_ERR_CAPACITY, "packed batch exceeds workspace capacity");
   hipStream_t st = stream ? as_stream(stream) : ws->stream;
-  return run_forward(ws, ids_dev, cu_seqlens_dev, n_seqs, total_tokens, max_seq_len ? max_seq_len : ae::kMaxPos,
-                     out_dev, st);
+  return run_forward_replay(ws, ids_dev, cu_seqlens_dev, n_seqs, total_tokens,
+                            max_seq_len ? max_seq_len : ae::kMaxPos, out_dev, st);
 }
 
 float ae_cosine_similarity(const float* a, const float* b) {  // src/lib.rs:265-271
@@ -702,6 +773,7 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   if (n_seqs == 0) return AE_OK;
   int* plan = nullptr;
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs, total_tokens) * sizeof(int)));
+  aek::init_attention_kernels();
   aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
                   aek::attention_pitch(ae::kMaxPos)};
   aek::launch_attention(a, aek::attention_max_tiles(n_seqs, total_tokens), as_stream(stream));
@@ -744,6 +816,12 @@ int ae_write_synthetic_ae8(const char* path, uint64_t seed) {
   if (!path) return fail(AE_ERR_INVALID_ARG, "null path");
   std::string err;
   if (int rc = ae::write_synthetic_ae8(path, seed, err)) return fail(rc, err);
+  return AE_OK;
+}
+
+int ae_workspace_set_graphs(ae_workspace* ws, int enabled) {
+  if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
+  ws->graphs = enabled != 0;
   return AE_OK;
 }
 

@@ -161,3 +161,32 @@ def test_layer_prefix_state(engine, ws, oracle_model, layers):
     print("layers %d: max |dh| %.3g, act_q mismatch %.2e, max |dq| %d, scale mismatch %d" % (
         layers, np.abs(h - rh).max(), flips, np.abs(q.astype(int) - rq).max(), int((sc != rsc).sum())), flush=True)
     assert np.array_equal(h, rh) and np.array_equal(q, rq) and np.array_equal(sc, rsc)
+
+
+def test_graph_replay_matches_eager(engine, oracle_model, torch_gpu):
+    """Repeated forward passes replay a captured hipGraph: every replay, interleaved with
+    eager passes of other shapes and host synchronizations, equals the eager result."""
+    torch = torch_gpu
+    seqs = ragged_batch(9, 3, 260, 41)
+    other = ragged_batch(5, 2, 90, 42)
+    lens = [len(s) for s in seqs]
+    T, B = int(sum(lens)), len(seqs)
+    ws = engine.workspace(4096, 64)
+    ids = torch.from_numpy(np.concatenate(seqs).view(np.int16)).cuda()
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).cuda()
+    out = torch.zeros((B, 384), dtype=torch.float32, device="cuda")
+    ws.set_graphs(False)
+    engine.forward_packed_device(ws, ids.data_ptr(), cu.data_ptr(), B, T, out.data_ptr(), ws.stream, max(lens))
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().copy()
+    ref = np.stack([oracle_model.forward_cls(s) for s in seqs])
+    assert np.array_equal(eager.view(np.uint32), ref.view(np.uint32))
+    ws.set_graphs(True)
+    for i in range(5):  # 1st call eager, 2nd captures, then replays
+        out.zero_()
+        torch.cuda.synchronize()
+        engine.forward_packed_device(ws, ids.data_ptr(), cu.data_ptr(), B, T, out.data_ptr(), ws.stream, max(lens))
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), eager.view(np.uint32)), i
+        engine.embed_batch_tokens(ws, other)  # other shapes through the same workspace in between
+    ws.close()
