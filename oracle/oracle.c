@@ -76,6 +76,8 @@ static void free_linear(or_linear* l) {
   free(l->w_scale);
   free(l->bias);
   free(l->inv_smooth);
+  free(l->xpack);
+  free(l->xcomp);
 }
 
 void or_free(or_model* m) {
@@ -333,8 +335,8 @@ void or_l2(float* v, int n) { /* src/simd_math.rs:2892-2903 */
   }
 }
 
-void or_attention_head(const float* qkv, int len, int stride, int q_off, int k_off, int v_off,
-                       float* ctx, int ctx_stride) {
+static void attention_head_k(const float* qkv, int len, int stride, int q_off, int k_off, int v_off,
+                             float* ctx, int ctx_stride, const or_kernels* K) {
   /* src/model.rs:663-694 for one (segment, head): copy K/V head rows, then per query
      compute_scores_head32 -> softmax_inplace -> weighted_sum_head32 */
   float* kh = (float*)malloc((size_t)(len ? len : 1) * 32 * sizeof(float));
@@ -346,11 +348,19 @@ void or_attention_head(const float* qkv, int len, int stride, int q_off, int k_o
     memcpy(vh + (size_t)t * 32, qkv + (size_t)t * stride + v_off, 32 * sizeof(float));
   }
   for (int tq = 0; tq < len; tq++) {
-    or_scores(qkv + (size_t)tq * stride + q_off, kh, inv_sqrt_d, sc, len);
-    or_softmax(sc, len);
-    or_wsum(sc, vh, len, ctx + (size_t)tq * ctx_stride);
+    K->scores(qkv + (size_t)tq * stride + q_off, kh, inv_sqrt_d, sc, len);
+    K->softmax(sc, len);
+    K->wsum(sc, vh, len, ctx + (size_t)tq * ctx_stride);
   }
   free(kh); free(vh); free(sc);
+}
+
+const or_kernels or_scalar_kernels = {or_gemm, or_ln_quant_row, or_smooth_quant_row, or_gelu_quant_row,
+                                      or_scores, or_softmax, or_wsum};
+
+void or_attention_head(const float* qkv, int len, int stride, int q_off, int k_off, int v_off,
+                       float* ctx, int ctx_stride) {
+  attention_head_k(qkv, len, stride, q_off, k_off, v_off, ctx, ctx_stride, &or_scalar_kernels);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -369,7 +379,7 @@ typedef struct {
   float* act_scale;
 } fwd_ws;
 
-static void embed_tokens(const or_model* m, const uint16_t* const* seq_ids, fwd_ws* w) {
+static void embed_tokens(const or_model* m, const uint16_t* const* seq_ids, fwd_ws* w, const or_kernels* K) {
   /* src/model.rs:549-586: local positions 0..len per segment */
   const float* first_inv_smooth = m->layers[0].qkv.inv_smooth;
   for (int b = 0; b < w->B; b++) {
@@ -379,7 +389,7 @@ static void embed_tokens(const or_model* m, const uint16_t* const* seq_ids, fwd_
       float* h_row = w->hidden + (size_t)gt * H;
       or_emb_row(m->word_q + (size_t)tok * H, m->word_s[tok], m->pos_q + (size_t)lt * H,
                  m->pos_s[lt], m->type0, h_row, H);
-      w->act_scale[gt] = or_ln_quant_row(h_row, m->emb_ln_w, m->emb_ln_b, first_inv_smooth,
+      w->act_scale[gt] = K->ln_quant_row(h_row, m->emb_ln_w, m->emb_ln_b, first_inv_smooth,
                                          w->act_q + (size_t)gt * H, H, OR_LN_EPS);
     }
   }
@@ -387,45 +397,45 @@ static void embed_tokens(const or_model* m, const uint16_t* const* seq_ids, fwd_
 
 static void swap_f(float** a, float** b) { float* t = *a; *a = *b; *b = t; }
 
-static void full_layer(const or_model* m, int l, fwd_ws* w, int quant_next) {
+static void full_layer(const or_model* m, int l, fwd_ws* w, int quant_next, const or_kernels* K) {
   /* one layer over all T rows: src/model.rs:593-767 */
   const or_layer* L = &m->layers[l];
   const int T = w->T;
-  or_gemm(T, w->act_q, w->act_scale, &L->qkv, NULL, w->qkv);
+  K->gemm(T, w->act_q, w->act_scale, &L->qkv, NULL, w->qkv);
   for (int b = 0; b < w->B; b++)
     for (int h = 0; h < OR_HEADS; h++) {
       const int ho = h * 32;
-      or_attention_head(w->qkv + (size_t)w->seg_start[b] * 3 * H, w->seg_len[b], 3 * H, ho, H + ho,
-                        2 * H + ho, w->ctx + (size_t)w->seg_start[b] * H + ho, H);
+      attention_head_k(w->qkv + (size_t)w->seg_start[b] * 3 * H, w->seg_len[b], 3 * H, ho, H + ho,
+                       2 * H + ho, w->ctx + (size_t)w->seg_start[b] * H + ho, H, K);
     }
   for (int t = 0; t < T; t++)
-    w->act_scale[t] = or_smooth_quant_row(w->ctx + (size_t)t * H, L->attn_out.inv_smooth,
+    w->act_scale[t] = K->smooth_quant_row(w->ctx + (size_t)t * H, L->attn_out.inv_smooth,
                                           w->act_q + (size_t)t * H, H);
-  or_gemm(T, w->act_q, w->act_scale, &L->attn_out, w->hidden, w->tmp);
+  K->gemm(T, w->act_q, w->act_scale, &L->attn_out, w->hidden, w->tmp);
   swap_f(&w->hidden, &w->tmp);
   for (int t = 0; t < T; t++)
-    w->act_scale[t] = or_ln_quant_row(w->hidden + (size_t)t * H, L->ln1_w, L->ln1_b,
+    w->act_scale[t] = K->ln_quant_row(w->hidden + (size_t)t * H, L->ln1_w, L->ln1_b,
                                       L->ffn_inter.inv_smooth, w->act_q + (size_t)t * H, H, OR_LN_EPS);
-  or_gemm(T, w->act_q, w->act_scale, &L->ffn_inter, NULL, w->inter);
+  K->gemm(T, w->act_q, w->act_scale, &L->ffn_inter, NULL, w->inter);
   for (int t = 0; t < T; t++)
-    w->act_scale[t] = or_gelu_quant_row(w->inter + (size_t)t * I, L->ffn_out.inv_smooth,
+    w->act_scale[t] = K->gelu_quant_row(w->inter + (size_t)t * I, L->ffn_out.inv_smooth,
                                         w->inter_q + (size_t)t * I, I);
-  or_gemm(T, w->inter_q, w->act_scale, &L->ffn_out, w->hidden, w->tmp);
+  K->gemm(T, w->inter_q, w->act_scale, &L->ffn_out, w->hidden, w->tmp);
   swap_f(&w->hidden, &w->tmp);
   if (quant_next) {
     const float* next_smooth = m->layers[l + 1].qkv.inv_smooth;
     for (int t = 0; t < T; t++)
-      w->act_scale[t] = or_ln_quant_row(w->hidden + (size_t)t * H, L->ln2_w, L->ln2_b, next_smooth,
+      w->act_scale[t] = K->ln_quant_row(w->hidden + (size_t)t * H, L->ln2_w, L->ln2_b, next_smooth,
                                         w->act_q + (size_t)t * H, H, OR_LN_EPS);
   }
 }
 
-static void last_layer_pruned(const or_model* m, fwd_ws* w, float* out) {
+static void last_layer_pruned(const or_model* m, fwd_ws* w, float* out, const or_kernels* K) {
   /* src/model.rs:770-913 */
   const or_layer* L = &m->layers[OR_LAYERS - 1];
   const int T = w->T, B = w->B;
   float* kv = (float*)malloc((size_t)T * 2 * H * sizeof(float));
-  or_gemm(T, w->act_q, w->act_scale, &L->kv_only, NULL, kv);
+  K->gemm(T, w->act_q, w->act_scale, &L->kv_only, NULL, kv);
   /* compact CLS rows to 0..B (:787-800); forward order keeps it in-place safe */
   for (int b = 0; b < B; b++) {
     const int cls_t = w->seg_start[b];
@@ -436,7 +446,7 @@ static void last_layer_pruned(const or_model* m, fwd_ws* w, float* out) {
     }
   }
   float* q_cls = (float*)malloc((size_t)B * H * sizeof(float));
-  or_gemm(B, w->act_q, w->act_scale, &L->q_only, NULL, q_cls);
+  K->gemm(B, w->act_q, w->act_scale, &L->q_only, NULL, q_cls);
   const float inv_sqrt_d = 1.0f / sqrtf(32.0f);
   float* kh = (float*)malloc((size_t)OR_MAX_POS * 32 * sizeof(float));
   float* vh = (float*)malloc((size_t)OR_MAX_POS * 32 * sizeof(float));
@@ -449,23 +459,23 @@ static void last_layer_pruned(const or_model* m, fwd_ws* w, float* out) {
         memcpy(kh + (size_t)lt * 32, kv + (size_t)(s0 + lt) * 2 * H + ho, 32 * sizeof(float));
         memcpy(vh + (size_t)lt * 32, kv + (size_t)(s0 + lt) * 2 * H + H + ho, 32 * sizeof(float));
       }
-      or_scores(q_cls + (size_t)b * H + ho, kh, inv_sqrt_d, sc, len);
-      or_softmax(sc, len);
-      or_wsum(sc, vh, len, w->ctx + (size_t)b * H + ho);
+      K->scores(q_cls + (size_t)b * H + ho, kh, inv_sqrt_d, sc, len);
+      K->softmax(sc, len);
+      K->wsum(sc, vh, len, w->ctx + (size_t)b * H + ho);
     }
   }
   for (int b = 0; b < B; b++) /* :846-852 */
-    w->act_scale[b] = or_smooth_quant_row(w->ctx + (size_t)b * H, L->attn_out.inv_smooth,
+    w->act_scale[b] = K->smooth_quant_row(w->ctx + (size_t)b * H, L->attn_out.inv_smooth,
                                           w->act_q + (size_t)b * H, H);
-  or_gemm(B, w->act_q, w->act_scale, &L->attn_out, w->hidden, w->tmp);
+  K->gemm(B, w->act_q, w->act_scale, &L->attn_out, w->hidden, w->tmp);
   for (int b = 0; b < B; b++)
-    w->act_scale[b] = or_ln_quant_row(w->tmp + (size_t)b * H, L->ln1_w, L->ln1_b,
+    w->act_scale[b] = K->ln_quant_row(w->tmp + (size_t)b * H, L->ln1_w, L->ln1_b,
                                       L->ffn_inter.inv_smooth, w->act_q + (size_t)b * H, H, OR_LN_EPS);
-  or_gemm(B, w->act_q, w->act_scale, &L->ffn_inter, NULL, w->inter);
+  K->gemm(B, w->act_q, w->act_scale, &L->ffn_inter, NULL, w->inter);
   for (int b = 0; b < B; b++)
-    w->act_scale[b] = or_gelu_quant_row(w->inter + (size_t)b * I, L->ffn_out.inv_smooth,
+    w->act_scale[b] = K->gelu_quant_row(w->inter + (size_t)b * I, L->ffn_out.inv_smooth,
                                         w->inter_q + (size_t)b * I, I);
-  or_gemm(B, w->inter_q, w->act_scale, &L->ffn_out, w->tmp, w->hidden);
+  K->gemm(B, w->inter_q, w->act_scale, &L->ffn_out, w->tmp, w->hidden);
   for (int b = 0; b < B; b++) {
     float* row = w->hidden + (size_t)b * H;
     or_ln_row(row, L->ln2_w, L->ln2_b, H, OR_LN_EPS);
@@ -495,8 +505,8 @@ static void fwd_free(fwd_ws* w) {
 }
 
 /* runs one packed batch of B segments (already truncated) */
-static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, const int* lens, int B,
-                          int prune, float* out) {
+static int forward_packed_k(const or_model* m, const uint16_t* const* seq_ids, const int* lens, int B,
+                            int prune, float* out, const or_kernels* K) {
   int* starts = (int*)malloc(sizeof(int) * (B > 0 ? B : 1));
   int T = 0;
   for (int b = 0; b < B; b++) {
@@ -509,10 +519,10 @@ static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, con
   fwd_ws w = {0};
   w.T = T; w.B = B; w.seg_start = starts; w.seg_len = lens;
   if (fwd_alloc(&w, T)) { fwd_free(&w); free(starts); return OR_ERR_ARG; }
-  embed_tokens(m, seq_ids, &w);
-  for (int l = 0; l < OR_LAYERS - 1; l++) full_layer(m, l, &w, 1);
+  embed_tokens(m, seq_ids, &w, K);
+  for (int l = 0; l < OR_LAYERS - 1; l++) full_layer(m, l, &w, 1, K);
   if (prune) {
-    last_layer_pruned(m, &w, out);
+    last_layer_pruned(m, &w, out, K);
   } else {
     /* unpruned layer 11: the full QKV of layer 11 is q_only rows ++ kv_only rows */
     const or_layer* L = &m->layers[OR_LAYERS - 1];
@@ -533,7 +543,7 @@ static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, con
     m2.layers[OR_LAYERS - 1].qkv.w_q = full.w_q;
     m2.layers[OR_LAYERS - 1].qkv.w_scale = full.w_scale;
     m2.layers[OR_LAYERS - 1].qkv.bias = full.bias;
-    full_layer(&m2, OR_LAYERS - 1, &w, 0);
+    full_layer(&m2, OR_LAYERS - 1, &w, 0, K);
     for (int b = 0; b < B; b++) {
       float* row = w.hidden + (size_t)starts[b] * H;
       or_ln_row(row, L->ln2_w, L->ln2_b, H, OR_LN_EPS);
@@ -547,11 +557,20 @@ static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, con
   return OR_OK;
 }
 
-int or_forward_cls(const or_model* m, const uint16_t* ids, size_t n, float* out384) {
+static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, const int* lens, int B,
+                          int prune, float* out) {
+  return forward_packed_k(m, seq_ids, lens, B, prune, out, &or_scalar_kernels);
+}
+
+static int forward_cls_k(const or_model* m, const uint16_t* ids, size_t n, float* out384, const or_kernels* K) {
   /* src/model.rs:191-192: seq_len = min(len, 512); empty input is rejected */
   int len = (int)(n < OR_MAX_POS ? n : OR_MAX_POS);
   if (len < 1) return OR_ERR_ARG;
-  return forward_packed(m, &ids, &len, 1, 1, out384);
+  return forward_packed_k(m, &ids, &len, 1, 1, out384, K);
+}
+
+int or_forward_cls(const or_model* m, const uint16_t* ids, size_t n, float* out384) {
+  return forward_cls_k(m, ids, n, out384, &or_scalar_kernels);
 }
 
 int or_forward_cls_unpruned(const or_model* m, const uint16_t* ids, size_t n, float* out384) {
@@ -560,10 +579,10 @@ int or_forward_cls_unpruned(const or_model* m, const uint16_t* ids, size_t n, fl
   return forward_packed(m, &ids, &len, 1, 0, out384);
 }
 
-int or_forward_ragged_cls(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
-                          float* out) {
+static int forward_ragged_cls_k(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
+                                float* out, const or_kernels* K) {
   if (b == 0) return OR_OK; /* src/model.rs:529-531 */
-  if (b == 1) return or_forward_cls(m, ids + offsets[0], offsets[1] - offsets[0], out);
+  if (b == 1) return forward_cls_k(m, ids + offsets[0], offsets[1] - offsets[0], out, K);
   if (b > 64) return OR_ERR_ARG; /* :540-543 */
   const uint16_t* seqs[64];
   int lens[64];
@@ -576,7 +595,12 @@ int or_forward_ragged_cls(const or_model* m, const uint16_t* ids, const uint32_t
     seqs[i] = ids + offsets[i];
     cursor += lens[i];
   }
-  return forward_packed(m, seqs, lens, b, 1, out);
+  return forward_packed_k(m, seqs, lens, b, 1, out, K);
+}
+
+int or_forward_ragged_cls(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
+                          float* out) {
+  return forward_ragged_cls_k(m, ids, offsets, b, out, &or_scalar_kernels);
 }
 
 int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
@@ -598,8 +622,8 @@ int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offset
   fwd_ws w = {0};
   w.T = T; w.B = b; w.seg_start = starts; w.seg_len = lens;
   fwd_alloc(&w, T);
-  embed_tokens(m, seqs, &w);
-  for (int l = 0; l < upto_layer; l++) full_layer(m, l, &w, 1);
+  embed_tokens(m, seqs, &w, &or_scalar_kernels);
+  for (int l = 0; l < upto_layer; l++) full_layer(m, l, &w, 1, &or_scalar_kernels);
   memcpy(hidden, w.hidden, (size_t)T * H * 4);
   memcpy(act_q, w.act_q, (size_t)T * H);
   memcpy(act_scale, w.act_scale, (size_t)T * 4);
@@ -618,13 +642,14 @@ typedef struct {
   const uint32_t* offsets;
   size_t n;
   float* out;
+  const or_kernels* k;
   atomic_size_t next;
   atomic_int err;
 } batch_job;
 
 static int run_single(batch_job* j, size_t idx) {
-  return or_forward_cls(j->m, j->ids + j->offsets[idx], j->offsets[idx + 1] - j->offsets[idx],
-                        j->out + idx * H);
+  return forward_cls_k(j->m, j->ids + j->offsets[idx], j->offsets[idx + 1] - j->offsets[idx],
+                       j->out + idx * H, j->k);
 }
 
 static void* batch_worker(void* arg) {
@@ -667,7 +692,7 @@ static void* batch_worker(void* arg) {
         offs[k + 1] = offs[k] + (uint32_t)ln;
       }
       float staging[4 * H];
-      int rc = or_forward_ragged_cls(j->m, buf, offs, (int)pack_count, staging);
+      int rc = forward_ragged_cls_k(j->m, buf, offs, (int)pack_count, staging, j->k);
       if (rc) atomic_store(&j->err, rc);
       for (size_t k = 0; k < pack_count; k++)
         memcpy(j->out + idxs[k] * H, staging + k * H, H * sizeof(float));
@@ -678,11 +703,16 @@ static void* batch_worker(void* arg) {
 
 int or_embed_batch_tokens(const or_model* m, const uint16_t* ids, const uint32_t* offsets, size_t n,
                           int num_threads, float* out) {
+  return or_embed_batch_tokens_k(m, ids, offsets, n, num_threads, out, &or_scalar_kernels);
+}
+
+int or_embed_batch_tokens_k(const or_model* m, const uint16_t* ids, const uint32_t* offsets, size_t n,
+                            int num_threads, float* out, const or_kernels* k) {
   if (n == 0) return OR_OK; /* :145-147 */
   size_t threads = num_threads < 1 ? 1 : (size_t)num_threads;
   if (threads > n) threads = n;
   batch_job j;
-  j.m = m; j.ids = ids; j.offsets = offsets; j.n = n; j.out = out;
+  j.m = m; j.ids = ids; j.offsets = offsets; j.n = n; j.out = out; j.k = k;
   atomic_init(&j.next, 0);
   atomic_init(&j.err, 0);
   if (threads == 1) {

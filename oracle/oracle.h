@@ -47,6 +47,8 @@ typedef struct {
   float* w_scale;
   float* bias;
   float* inv_smooth;
+  int8_t* xpack;  /* x86 CPU baseline only: weights in pack_weights_x86 order, else NULL */
+  int32_t* xcomp; /* x86 CPU baseline only: -128 * row sums (VNNI col_sum_comp), else NULL */
 } or_linear;
 
 /* QuantizedLayerRaw (src/quantize.rs:47-59) */
@@ -118,6 +120,36 @@ void or_l2(float* v, int n);
    (src/model.rs:663-694 restricted to one head) */
 void or_attention_head(const float* qkv, int len, int stride, int q_off, int k_off,
                        int v_off, float* ctx, int ctx_stride);
+
+/* ---- backend kernel table ------------------------------------------------
+ * The drivers below (src/model.rs forward passes, src/lib.rs embed_batch) call
+ * their row / GEMM / attention kernels through this table, as the reference
+ * dispatches per SimdBackend (src/gemm.rs:630-671, src/simd_math.rs dispatchers).
+ * or_scalar_kernels is the oracle; oracle/x86.c provides the reference's x86
+ * backend for the CPU baseline. */
+typedef struct {
+  void (*gemm)(int m, const int8_t* a, const float* a_scale, const or_linear* w, const float* res, float* out);
+  float (*ln_quant_row)(float* x, const float* gamma, const float* beta, const float* inv_smooth, int8_t* q,
+                        int n, float eps);
+  float (*smooth_quant_row)(const float* x, const float* inv_smooth, int8_t* q, int n);
+  float (*gelu_quant_row)(float* x, const float* inv_smooth, int8_t* q, int n);
+  void (*scores)(const float* q, const float* k_head, float scale, float* scores, int len);
+  void (*softmax)(float* s, int len);
+  void (*wsum)(const float* p, const float* v_head, int len, float* out32);
+} or_kernels;
+extern const or_kernels or_scalar_kernels;
+/* oracle/x86.c: the reference's x86 backend, used as the CPU baseline.
+ * or_x86_backend: 2 AVX-VNNI, 1 AVX2+FMA, 0 none (src/gemm.rs:100-125).
+ * or_x86_prepare packs every linear (pack_weights_x86, col_sum_comp). */
+int or_x86_backend(void);
+int or_x86_prepare(or_model* m);
+int or_x86_embed_batch_tokens(const or_model* m, const uint16_t* ids, const uint32_t* offsets, size_t n,
+                              int num_threads, float* out);
+int or_x86_gemm(int m, const int8_t* a, const float* a_scale, or_linear* w, const float* res, float* out,
+                int variant);
+/* embed_batch over ids with an explicit backend table */
+int or_embed_batch_tokens_k(const or_model* m, const uint16_t* ids, const uint32_t* offsets, size_t n,
+                            int num_threads, float* out, const or_kernels* k);
 
 /* ---- drivers ------------------------------------------------------------ */
 /* PackedModel::forward_cls, src/model.rs:185-513 */

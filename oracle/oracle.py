@@ -24,7 +24,8 @@ _fp = ctypes.POINTER(ctypes.c_float)
 class _Linear(ctypes.Structure):
     _fields_ = [("n_out", ctypes.c_uint64), ("k_in", ctypes.c_uint64), ("w_len", ctypes.c_uint64),
                 ("s_len", ctypes.c_uint64), ("b_len", ctypes.c_uint64), ("is_len", ctypes.c_uint64),
-                ("w_q", ctypes.POINTER(ctypes.c_int8)), ("w_scale", _fp), ("bias", _fp), ("inv_smooth", _fp)]
+                ("w_q", ctypes.POINTER(ctypes.c_int8)), ("w_scale", _fp), ("bias", _fp), ("inv_smooth", _fp),
+                ("xpack", ctypes.POINTER(ctypes.c_int8)), ("xcomp", ctypes.POINTER(ctypes.c_int32))]
 
 
 class _Layer(ctypes.Structure):
@@ -71,6 +72,10 @@ _sigs = {
     "or_forward_cls_unpruned": (ctypes.c_int, [_MP, _vp, ctypes.c_size_t, _vp]),
     "or_forward_ragged_cls": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, _vp]),
     "or_embed_batch_tokens": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
+    "or_x86_backend": (ctypes.c_int, []),
+    "or_x86_gemm": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.POINTER(_Linear), _vp, _vp, ctypes.c_int]),
+    "or_x86_prepare": (ctypes.c_int, [_MP]),
+    "or_x86_embed_batch_tokens": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
     "or_run_prefix": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
 }
 for _n, (_r, _a) in _sigs.items():
@@ -100,6 +105,36 @@ class LinearView:
         self.w_scale = _arr(lin.w_scale, lin.s_len, np.float32)
         self.bias = _arr(lin.bias, lin.b_len, np.float32)
         self.inv_smooth = _arr(lin.inv_smooth, lin.is_len, np.float32)
+
+
+def x86_gemm(a_q, a_scale, w_q, w_scale, bias, res=None, variant=1):
+    """The x86 baseline's GEMM (variant 1: AVX2 maddubs, 2: AVX-VNNI) on the same operands as gemm()."""
+    a_q = np.ascontiguousarray(a_q, dtype=np.int8)
+    w_q = np.ascontiguousarray(w_q, dtype=np.int8)
+    m, k = a_q.shape
+    n = w_q.shape[0]
+    ws, b = _f32(w_scale), _f32(bias)
+    inv = np.ones(k, np.float32)
+    lin = _Linear(n, k, n * k, n, n, k, w_q.ctypes.data_as(ctypes.POINTER(ctypes.c_int8)),
+                  ws.ctypes.data_as(_fp), b.ctypes.data_as(_fp), inv.ctypes.data_as(_fp))
+    sc = _f32(a_scale)
+    out = np.zeros((m, n), np.float32)
+    r = None if res is None else _f32(res)
+    rc = _lib.or_x86_gemm(m, a_q.ctypes.data, sc.ctypes.data, ctypes.byref(lin),
+                          None if r is None else r.ctypes.data, out.ctypes.data, int(variant))
+    # the packed copies belong to this temporary linear
+    libc_free = ctypes.CDLL(None).free
+    libc_free.argtypes = [ctypes.c_void_p]
+    libc_free(ctypes.cast(lin.xpack, ctypes.c_void_p))
+    libc_free(ctypes.cast(lin.xcomp, ctypes.c_void_p))
+    if rc:
+        raise ValueError("or_x86_gemm: %d" % rc)
+    return out
+
+
+def x86_backend():
+    """The reference's x86 backend on this host: 'avx_vnni', 'avx2' or None (src/gemm.rs:100-125)."""
+    return {2: "avx_vnni", 1: "avx2"}.get(int(_lib.or_x86_backend()))
 
 
 def _pack(seqs):
@@ -181,6 +216,22 @@ class OracleModel:
                                         out.ctypes.data)
         if rc:
             raise ValueError("or_embed_batch_tokens: %d" % rc)
+        return out
+
+    def x86_embed_batch_tokens(self, seqs, num_threads=1):
+        """embed_batch on the restated x86 backend of the reference (AVX-VNNI or AVX2, chosen as the
+        reference chooses): the CPU baseline.  Not bit-identical to the scalar oracle."""
+        if not getattr(self, "_x86_ready", False):
+            rc = _lib.or_x86_prepare(self._m)
+            if rc:
+                raise ValueError("or_x86_prepare: %d (no AVX2+FMA?)" % rc)
+            self._x86_ready = True
+        ids, offs = _pack(seqs)
+        out = np.zeros((len(seqs), H), dtype=np.float32)
+        rc = _lib.or_x86_embed_batch_tokens(self._m, ids.ctypes.data, offs.ctypes.data, len(seqs), int(num_threads),
+                                            out.ctypes.data)
+        if rc:
+            raise ValueError("or_x86_embed_batch_tokens: %d" % rc)
         return out
 
     def run_prefix(self, seqs, upto_layer):

@@ -289,3 +289,39 @@ def test_truncation_and_empty(oracle_model):
     assert np.array_equal(oracle_model.forward_cls(ids), oracle_model.forward_cls(ids[:512]))
     with pytest.raises(ValueError):
         oracle_model.forward_cls(np.zeros(0, np.uint16))
+
+
+# ---- the CPU baseline: the reference's x86 backend (oracle/x86.c) -------------
+
+@pytest.mark.skipif(orc.x86_backend() is None, reason="host without AVX2+FMA")
+@pytest.mark.parametrize("n,k", [(1152, 384), (384, 1536), (768, 384)])
+def test_x86_gemm_equals_scalar_gemm(n, k):
+    """Both x86 GEMMs are exact in int32 and share the scalar epilogue: bit-identical outputs."""
+    rng = np.random.default_rng(n + k)
+    m = 37
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    a[0], w[0] = 127, -127  # extreme rows
+    sa = rng.uniform(0.01, 0.1, m).astype(np.float32)
+    ws = (0.05 / 127 * rng.uniform(0.5, 1.5, n)).astype(np.float32)
+    b = rng.normal(0, 0.02, n).astype(np.float32)
+    res = rng.normal(0, 1, (m, n)).astype(np.float32)
+    ref = orc.gemm(a, sa, w, ws, b, res)
+    variants = [1] + ([2] if orc.x86_backend() == "avx_vnni" else [])
+    for v in variants:
+        got = orc.x86_gemm(a, sa, w, ws, b, res, variant=v)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), v
+
+
+@pytest.mark.skipif(orc.x86_backend() is None, reason="host without AVX2+FMA")
+def test_x86_backend_tracks_scalar_backend(oracle_model):
+    """The x86 backend rounds its row / attention kernels differently from the scalar path;
+    the reference holds its backends to cosine > 0.999 of each other (tests/accuracy_test.rs:194-195)."""
+    rng = np.random.default_rng(77)
+    seqs = [np.concatenate([[101], rng.integers(1000, 30522, int(L) - 2), [102]]).astype(np.uint16)
+            for L in (3, 9, 14, 17, 40, 130)]
+    ref = oracle_model.embed_batch_tokens(seqs, 4)
+    got = oracle_model.x86_embed_batch_tokens(seqs, 4)
+    cos = (ref.astype(np.float64) * got).sum(1) / (np.linalg.norm(ref, axis=1) * np.linalg.norm(got, axis=1))
+    assert cos.min() > 0.999, cos
+    assert np.allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
