@@ -7,8 +7,10 @@ before the timed region; `value` is embeddings/s over exactly --steps passes.
 
 Also reported: per-kernel device time (HIP events on the workspace stream over
 the timed region) and the roofline of the dominant kernel, ms/seq at 128 tokens
-(configs[0]), and the CPU baseline: the oracle's restatement of the reference's
-scalar path under the reference's embed_batch policy on the host's cores.
+(configs[0]), the end-to-end roofline (the sum over launches of each kernel's
+ideal time against the measured pass), and the CPU baseline: the oracle's
+restatement of the reference's best x86 backend (AVX-VNNI, else AVX2) under the
+reference's embed_batch policy on the host's cores.
 """
 import argparse
 import json
@@ -62,6 +64,48 @@ def kernel_work(kind, T, B, lens):
     if kind == "embed_ln":  # gather 2 int8 rows + 2 scales, write f32 row + int8 row + scale
         return "GB/s", T * (2 * 384 + 8 + 384 * 4 + 384 + 4), "hbm", PEAK_HBM_GBS
     return None
+
+
+def roofline_step_ms(T, B, lens):
+    """Ideal time of one forward pass: the sum over launches of max(ops / peak, bytes / HBM) with
+    algorithmic ops and bytes (weights read once per launch), per kernel kind (ms per step)."""
+    sum_l2 = float(sum(int(L) * int(L) for L in lens))
+    hbm = PEAK_HBM_GBS * 1e9
+
+    def gemm(M, N, K, a_bytes, res):
+        ops = 2.0 * M * N * K
+        byts = a_bytes * M * K + 4 * M + N * K + 8 * N + 4 * M * N * (2 if res else 1)
+        return max(ops / (PEAK_INT8_TOPS * 1e12), byts / hbm)
+
+    per = {
+        "embed_ln": T * (2 + 2 * 384 + 8 + 384 * 4 + 384 + 4) / hbm,
+        "gemm_qkv": 11 * gemm(T, 1152, 384, 1, False),
+        "attention": 11 * max(4.0 * 12 * 32 * sum_l2 / (PEAK_FP32_TFLOPS * 1e12), T * (1152 + 384) * 4 / hbm),
+        "gemm_attn_out": 11 * gemm(T, 384, 384, 4, True),
+        "ln1": 11 * T * (384 * 4 * 2 + 384 + 4) / hbm,
+        "gemm_ffn_up": 11 * gemm(T, 1536, 384, 1, False),
+        "gemm_ffn_down": 11 * gemm(T, 384, 1536, 4, True),
+        "ln2": 11 * T * (384 * 4 * 2 + 384 + 4) / hbm,
+        # layer 11: K/V for all tokens, the [CLS] query's attention over them, then the B-row tail
+        "layer11_tail": gemm(T, 768, 384, 1, False) + T * 768 * 4 / hbm
+        + gemm(B, 384, 384, 1, False) + gemm(B, 384, 384, 4, True) + gemm(B, 1536, 384, 1, False)
+        + gemm(B, 384, 1536, 4, True) + 3 * B * 3460 / hbm,
+    }
+    return {k: v * 1e3 for k, v in per.items()}
+
+
+def host_cpu():
+    """The host's CPU model and the ISA extensions the reference's x86 dispatch looks at."""
+    model, flags = "unknown", set()
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name") and model == "unknown":
+                model = ln.split(":", 1)[1].strip()
+            elif ln.startswith("flags") and not flags:
+                flags = set(ln.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return model, [f for f in ("avx2", "fma", "avx_vnni", "avx512f", "avx512_vnni") if f in flags]
 
 
 def gemm_microbench(ae, torch, iters):
@@ -207,6 +251,11 @@ def main():
     roofline = {"kernel": dom, "bound": bound, "achieved": round(achieved, 3), "peak": peak,
                 "unit": unit, "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom, workload),
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "algorithmic_per_launch": amount}
+    # end-to-end: the sum of every kernel's roofline time against the measured pass
+    roof = roofline_step_ms(T, B, lens)
+    e2e = {"t_roof_ms": round(sum(roof.values()), 4), "t_measured_ms": round(ms_per_step, 4),
+           "frac": round(sum(roof.values()) / ms_per_step, 4),
+           "per_kernel_frac": {k: round(roof[k] / kernel_ms[k], 4) for k in roof if kernel_ms.get(k)}}
     # the FFN GEMMs' fraction of dense int8 MFMA peak (BASELINE metric, part 2)
     ffn = {}
     for k in ("gemm_ffn_up", "gemm_ffn_down"):
@@ -263,12 +312,25 @@ def main():
             ref = run(sample)
             times.append(time.perf_counter() - t0)
         cpu_s = sorted(times)[1]
+        # ms/seq at 128 tokens on one thread (configs[0]'s sequence; median of 5)
+        c1seq = make_batch(1, 128, 128, 1)
+        one = (lambda s: m.x86_embed_batch_tokens(s, 1)) if backend else (lambda s: m.embed_batch_tokens(s, 1))
+        one(c1seq)
+        t1 = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            one(c1seq)
+            t1.append(time.perf_counter() - t0)
+        cpu_c1_ms = sorted(t1)[2] * 1e3
         m.close()
         g = emb[: len(sample)].astype(np.float64)
         r = np.asarray(ref, np.float64)
         cos = float(((g * r).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(r, axis=1))).min())
+        cpu_model, isa = host_cpu()
         cpu = {"value": round(len(sample) / cpu_s, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
                "backend": backend or "scalar",
+               "tokens_per_s": round(sum(len(s) for s in sample) / cpu_s, 1),
+               "ms_per_seq_128_1thread": round(cpu_c1_ms, 3), "cpu_model": cpu_model, "isa": isa,
                "sample": "first %d sequences (%d tokens) of the %s batch, median of 3 runs; restatement of the "
                          "reference's %s backend under its embed_batch policy"
                          % (len(sample), sum(len(s) for s in sample), workload,
@@ -284,7 +346,7 @@ def main():
         "wall_s": round(wall, 4), "outputs_unit_norm": norms_ok,
         "ffn_int8_mfma_frac": ffn, "ms_per_seq_128": c1_ms,
         "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
-        "roofline": roofline, "cpu_baseline": cpu,
+        "roofline": roofline, "e2e_roofline": e2e, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     ws.close()
