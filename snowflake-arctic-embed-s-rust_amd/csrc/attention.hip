@@ -87,6 +87,13 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 // The tiles of one (sequence, head) share that head's K and V: with the
 // XCD-contiguous numbering (xcd_contiguous) they run on one XCD and hit in its L2.
 // grid: max_tiles * 12 workgroups; logical item = head * max_tiles + tile
+//
+// kWide: operands in float4 groups with four MFMA results live at a time (one
+// float4 load of K per 16 dims, one float4 LDS read of P per 16 keys, and four
+// back-to-back MFMAs before their adds), ~146 VGPRs.  Otherwise one MFMA result
+// at a time with scalar operands, 80 VGPRs: for short rows, where the score
+// tile leaves room for more waves than the wide variant's registers do.
+template <bool kWide>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kAttnQ];
@@ -108,14 +115,28 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   const ExpTab tb = exp_tab_regs();
   const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
 
-  // Q fragments: qf[qh][j] = Q[q0 + 16qh + lr][4j + lg] (rows past the segment clamped)
+  // Dims of the score products (MFMA j, block b): kWide: dim 16(j/4) + 4b + j%4,
+  // so each lane's operands for MFMAs 4c..4c+3 are one float4 (dims 16c + 4lg ..
+  // +3) and four consecutive MFMA results hold 16 consecutive dims; otherwise
+  // dim 4j + b.  load_dims gives a lane its 8 operands of one row.
+  constexpr int G = kWide ? 4 : 1;  // MFMA results live at a time
+  auto load_dims = [&](const float* row, float (&f)[8]) {
+    if constexpr (kWide) {
+      const float4* src = reinterpret_cast<const float4*>(row + 4 * lg);
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const float4 v = src[4 * c];
+        f[4 * c] = v.x; f[4 * c + 1] = v.y; f[4 * c + 2] = v.z; f[4 * c + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) f[j] = row[4 * j + lg];
+    }
+  };
+  // qf[qh] = the Q operands of query q0 + 16qh + lr (rows past the segment clamped)
   float qf[2][8];
 #pragma unroll
-  for (int qh = 0; qh < 2; qh++) {
-    const int qr = min(q0 + 16 * qh + lr, L - 1);
-#pragma unroll
-    for (int j = 0; j < 8; j++) qf[qh][j] = qkv[(size_t)qr * HQKV + 4 * j + lg];
-  }
+  for (int qh = 0; qh < 2; qh++) load_dims(qkv + (size_t)min(q0 + 16 * qh + lr, L - 1) * HQKV, qf[qh]);
 
   // phase 1: scores (dot32_f32 scalar order) and the row max.  Wave w takes the
   // 16-key blocks kb = w, w+4, ... with both query halves; A = K block, B = Q
@@ -127,16 +148,25 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   // expf(s - max).
   float mrow[2] = {-INFINITY, -INFINITY};
   const int nkb = (L + 15) >> 4;
-  const float* kcol = qkv + H + lg;
-  auto load_kf = [&](int kb, float (&kf)[8]) {
-    const float* src = kcol + (size_t)min(16 * kb + lr, L - 1) * HQKV;
-#pragma unroll
-    for (int j = 0; j < 8; j++) kf[j] = src[4 * j];
-  };
+  auto load_kf = [&](int kb, float (&kf)[8]) { load_dims(qkv + H + (size_t)min(16 * kb + lr, L - 1) * HQKV, kf); };
+  // The dot product starts from its first product instead of 0 + p_0: the two
+  // differ only in the sign of a zero sum, and a score's zero sign cannot change
+  // expf(s - max) (the row max is then a zero too, or s - max = -max).
   auto score_half = [&](int t, const float (&kf)[8], const float (&q)[8], float* srow, float& m) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[4];
 #pragma unroll
-    for (int j = 0; j < 8; j++) add_blocks(acc, mfma_products(kf[j], q[j]));
+    for (int c = 0; c < 8 / G; c++) {
+      v16f pr[G];
+#pragma unroll
+      for (int u = 0; u < G; u++) pr[u] = mfma_products(kf[G * c + u], q[G * c + u]);
+#pragma unroll
+      for (int blk = 0; blk < 4; blk++)  // dims 4Gc + G*blk + u, in order
+#pragma unroll
+        for (int u = 0; u < G; u++)
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            acc[i] = (c == 0 && blk == 0 && u == 0) ? pr[0][i] : acc[i] + pr[u][4 * blk + i];
+    }
     float4 sc;
     sc.x = acc[0] * kInvSqrtD;
     sc.y = acc[1] * kInvSqrtD;
@@ -232,28 +262,47 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   }
 
   // phase 6: ctx[q][d] = sum_t p_t * v_t,d in order, p_t = e_t * inv.  Wave w
-  // owns the 16 x 16 quadrant (query half w/2, dim half w%2); one MFMA covers
-  // 4 consecutive keys: A = P (query x key), B = V (key x dim).  Lane l ends with
-  // queries 16qh + 4lg + i at dim 16dh + lr.  V fragments come from global
-  // memory 16 keys ahead, into ping-pong registers.
+  // owns the 16 x 16 quadrant (query half w/2, dim half w%2): A = P (query x
+  // key), B = V (key x dim).  In a group of 16 keys from t0, MFMA u, block b
+  // multiplies key t0 + 4b + u (kWide: each lane reads its four p operands as
+  // one float4, keys t0 + 4lg .. +3, and the four results are added key by key)
+  // or key t0 + 4u + b (one MFMA result at a time).
+  // Lane l ends with queries 16qh + 4lg + i at dim 16dh + lr.  V fragments come
+  // from global memory through a register ring.
   __syncthreads();  // publishes s_inv
   const int qh = wave >> 1, dh = wave & 1;
   const bool has_item = qh < nqh;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (has_item) {
-    const float* prow = &S[(16 * qh + lr) * pitch + lg];
+    const float* prow = &S[(16 * qh + lr) * pitch];
     const float inv = s_inv[16 * qh + lr];
-    const int voff = lg * HQKV + 2 * H + 16 * dh + lr;  // lane part of the V fragment address
+    const int vcol = 2 * H + 16 * dh + lr;
+    const int voff = (kWide ? 4 * lg : lg) * HQKV + vcol;  // lane part of the V fragment address
     // full groups of 16 keys: no masking; group starts of the prefetch are
     // clamped to the last full group (wave-uniform)
     const int Lf = L & ~15;
     auto load_v = [&](int t0, float (&v)[4]) {
 #pragma unroll
-      for (int u = 0; u < 4; u++) v[u] = (qkv + (size_t)(t0 + 4 * u) * HQKV)[voff];
+      for (int u = 0; u < 4; u++) v[u] = (qkv + (size_t)(t0 + (kWide ? u : 4 * u)) * HQKV)[voff];
     };
     auto pv_group = [&](int t0, const float (&v)[4]) {
+      if constexpr (kWide) {
+        const float4 e4 = *reinterpret_cast<const float4*>(prow + t0 + 4 * lg);
+        v16f pr[4];
+        pr[0] = mfma_products(e4.x * inv, v[0]);
+        pr[1] = mfma_products(e4.y * inv, v[1]);
+        pr[2] = mfma_products(e4.z * inv, v[2]);
+        pr[3] = mfma_products(e4.w * inv, v[3]);
 #pragma unroll
-      for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[t0 + 4 * u] * inv, v[u]));
+        for (int blk = 0; blk < 4; blk++)
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = acc[i] + pr[u][4 * blk + i];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[t0 + 4 * u + lg] * inv, v[u]));
+      }
     };
     // 4-deep register ring: each group's V is requested 48 keys ahead
     float v0[4], v1[4], v2[4], v3[4];
@@ -279,8 +328,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     for (int t0 = Lf; t0 < L; t0 += 4) {
       const int t = t0 + lg;
       const bool in = t < L;
-      const float e = prow[min(t, L - 1) - lg];
-      const float v = (qkv + (size_t)min(t, L - 1) * HQKV)[voff - lg * HQKV];
+      const float e = prow[min(t, L - 1)];
+      const float v = (qkv + (size_t)min(t, L - 1) * HQKV)[vcol];
       add_blocks(acc, mfma_products(in ? e * inv : 0.0f, in ? v : 0.0f));
     }
   }
@@ -323,15 +372,28 @@ int attention_pitch(int max_len) {
 // allow > 64 KiB of dynamic LDS for the tiled kernel on the current device; called
 // at engine open and by the stand-alone operator, never inside a stream capture
 void init_attention_kernels() {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)attention_lds_bytes(attention_pitch(512)));
+  const int lds = (int)attention_lds_bytes(attention_pitch(512));
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
-void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st) {
+// The wide variant (3 workgroups per CU by registers) is faster from rows of
+// about 64 keys up; batches of mostly shorter rows, whose workgroups are short
+// and latency-bound, run faster with the narrow one's 6.  The choice is by the
+// batch's mean length (both variants give the same bits).
+constexpr int kWideMinMeanLen = 48;
+
+void launch_attention(const AttnArgs& p, int T, hipStream_t st) {
   hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
-  if (max_tiles > 0)
-    hipLaunchKernelGGL(attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p,
-                       max_tiles);
+  const int max_tiles = attention_max_tiles(p.B, T);
+  if (T <= 0 || p.B <= 0) return;
+  const size_t lds = attention_lds_bytes(p.s_pitch);
+  if (T > kWideMinMeanLen * p.B)
+    hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
+  else
+    hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
 }
 
 // ---------------------------------------------------------------------------

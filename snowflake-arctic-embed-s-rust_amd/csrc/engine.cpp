@@ -343,7 +343,6 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.rowmax_init = ws->rowmax_ctx;
     launch_ln_quant(p, kLnSrcEmb, st);
   }
-  const int max_tiles = attention_max_tiles(B, T);
   const int s_pitch = attention_pitch(max_len);
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
@@ -355,7 +354,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
-      launch_attention(a, max_tiles, st);
+      launch_attention(a, T, st);
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
@@ -776,7 +775,7 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   aek::init_attention_kernels();
   aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
                   aek::attention_pitch(ae::kMaxPos)};
-  aek::launch_attention(a, aek::attention_max_tiles(n_seqs, total_tokens), as_stream(stream));
+  aek::launch_attention(a, total_tokens, as_stream(stream));
   hipError_t err = hipStreamSynchronize(as_stream(stream));
   (void)hipFree(plan);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));

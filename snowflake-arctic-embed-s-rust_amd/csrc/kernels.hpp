@@ -80,7 +80,7 @@ inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
 // ints of `plan` scratch for B segments and T tokens: tile prefix [B+1] + tile_seg [max_tiles]
 inline size_t attention_plan_ints(int B, int T) { return (size_t)B + 1 + attention_max_tiles(B, T); }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
-void launch_attention(const AttnArgs& p, int max_tiles, hipStream_t st);
+void launch_attention(const AttnArgs& p, int T, hipStream_t st);  // T = total tokens of the batch
 // test hook: raw results of the exact-product MFMA (16 floats per lane per set of 64 pairs)
 void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st);
 

@@ -183,10 +183,16 @@ def test_gelu_bit_exact_over_float_sample(torch_gpu):
     assert np.array_equal(bits(y)[~nan], bits(ref)[~nan])
 
 
-def test_attention_bit_exact(torch_gpu):
+# the attention kernel has two operand layouts, chosen by the batch's mean length
+# (48): these length sets reach both
+ATTN_LENS = {"mean81": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
+             "mean17": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8]}
+
+
+@pytest.mark.parametrize("lens", list(ATTN_LENS.values()), ids=list(ATTN_LENS))
+def test_attention_bit_exact(torch_gpu, lens):
     """Segment-bounded attention in the reference's scalar order: bit-exact."""
     torch = torch_gpu
-    lens = [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     T = int(cu[-1])
     rng = np.random.default_rng(21)
@@ -230,10 +236,10 @@ def test_mfma_products_equal_rounded_products(torch_gpu):
     assert np.count_nonzero((ref != 0) & (np.abs(ref) < np.finfo(f32).tiny)) > 1000  # denormals were covered
 
 
-def test_attention_bit_exact_extreme_magnitudes(torch_gpu):
+@pytest.mark.parametrize("lens", [[5, 40, 97, 300], [5, 40, 19, 33, 1]], ids=["mean110", "mean20"])
+def test_attention_bit_exact_extreme_magnitudes(torch_gpu, lens):
     """Scores and PV terms with denormal products, exact zeros and huge dynamic range."""
     torch = torch_gpu
-    lens = [5, 40, 97, 300]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     T = int(cu[-1])
     rng = np.random.default_rng(23)
