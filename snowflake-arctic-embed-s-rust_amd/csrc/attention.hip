@@ -277,18 +277,29 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     const float* prow = &S[(16 * qh + lr) * pitch];
     const float inv = s_inv[16 * qh + lr];
     const int vcol = 2 * H + 16 * dh + lr;
-    const int voff = (kWide ? 4 * lg : lg) * HQKV + vcol;  // lane part of the V fragment address
-    // full groups of 16 keys: no masking; group starts of the prefetch are
-    // clamped to the last full group (wave-uniform)
-    const int Lf = L & ~15;
-    auto load_v = [&](int t0, float (&v)[4]) {
+    // lane part of the V fragment offset (32-bit, from the segment's base)
+    const uint32_t voff = (uint32_t)((kWide ? 4 * lg : lg) * HQKV + vcol);
+    // full groups of 16 keys: no masking.  Group g's V goes to a 4-deep register
+    // ring three groups ahead and its P one group ahead; loads past the last full
+    // group are clamped to it (wave-uniform), so every load is unconditional and
+    // the main loop has no early exit.
+    const int Lf = L & ~15, ng = Lf >> 4;
+    auto load_v = [&](int g, float (&v)[4]) {
+      const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
 #pragma unroll
-      for (int u = 0; u < 4; u++) v[u] = (qkv + (size_t)(t0 + (kWide ? u : 4 * u)) * HQKV)[voff];
+      for (int u = 0; u < 4; u++) v[u] = qkv[(t0 + (kWide ? u : 4 * u)) * (uint32_t)HQKV + voff];
     };
-    auto pv_group = [&](int t0, const float (&v)[4]) {
+    auto load_p = [&](int g) {
+      const float* e = prow + 16 * min(g, ng - 1);
       if constexpr (kWide) {
-        const float4 e4 = *reinterpret_cast<const float4*>(prow + t0 + 4 * lg);
-        v16f pr[4];
+        return *reinterpret_cast<const float4*>(e + 4 * lg);  // keys t0 + 4lg .. +3
+      } else {
+        return float4{e[lg], e[4 + lg], e[8 + lg], e[12 + lg]};  // keys t0 + 4u + lg
+      }
+    };
+    auto pv_group = [&](const float4& e4, const float (&v)[4]) {
+      v16f pr[4];
+      if constexpr (kWide) {
         pr[0] = mfma_products(e4.x * inv, v[0]);
         pr[1] = mfma_products(e4.y * inv, v[1]);
         pr[2] = mfma_products(e4.z * inv, v[2]);
@@ -300,29 +311,74 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[i] = acc[i] + pr[u][4 * blk + i];
       } else {
-#pragma unroll
-        for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[t0 + 4 * u + lg] * inv, v[u]));
+        add_blocks(acc, mfma_products(e4.x * inv, v[0]));
+        add_blocks(acc, mfma_products(e4.y * inv, v[1]));
+        add_blocks(acc, mfma_products(e4.z * inv, v[2]));
+        add_blocks(acc, mfma_products(e4.w * inv, v[3]));
       }
     };
-    // 4-deep register ring: each group's V is requested 48 keys ahead
-    float v0[4], v1[4], v2[4], v3[4];
-    if (Lf > 0) {
+    if (!kWide) {
+      // one group per step through the ring (fewer registers, for short rows)
+      auto load_vn = [&](int g, float (&v)[4]) {
+        const float* src = qkv + (size_t)(16 * min(g, ng - 1)) * HQKV + voff;
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = src[(size_t)(4 * u) * HQKV];
+      };
+      auto pv_narrow = [&](int g, const float (&v)[4]) {  // P read as the MFMAs go
+#pragma unroll
+        for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[16 * g + 4 * u + lg] * inv, v[u]));
+      };
+      float v0[4], v1[4], v2[4], v3[4];
+      if (ng > 0) {
+        load_vn(0, v0);
+        load_vn(1, v1);
+        load_vn(2, v2);
+      }
+      for (int g = 0; g < ng; g += 4) {
+        load_vn(g + 3, v3);
+        pv_narrow(g, v0);
+        if (g + 1 >= ng) break;
+        load_vn(g + 4, v0);
+        pv_narrow(g + 1, v1);
+        if (g + 2 >= ng) break;
+        load_vn(g + 5, v1);
+        pv_narrow(g + 2, v2);
+        if (g + 3 >= ng) break;
+        load_vn(g + 6, v2);
+        pv_narrow(g + 3, v3);
+      }
+    } else if (ng > 0) {
+      float v0[4], v1[4], v2[4], v3[4];
+      float4 pa, pb;
       load_v(0, v0);
-      load_v(min(16, Lf - 16), v1);
-      load_v(min(32, Lf - 16), v2);
-    }
-    for (int t0 = 0; t0 < Lf; t0 += 64) {
-      load_v(min(t0 + 48, Lf - 16), v3);
-      pv_group(t0, v0);
-      if (t0 + 16 >= Lf) break;
-      load_v(min(t0 + 64, Lf - 16), v0);
-      pv_group(t0 + 16, v1);
-      if (t0 + 32 >= Lf) break;
-      load_v(min(t0 + 80, Lf - 16), v1);
-      pv_group(t0 + 32, v2);
-      if (t0 + 48 >= Lf) break;
-      load_v(min(t0 + 96, Lf - 16), v2);
-      pv_group(t0 + 48, v3);
+      load_v(1, v1);
+      load_v(2, v2);
+      pa = load_p(0);
+      int g = 0;
+      for (; g + 4 <= ng; g += 4) {
+        load_v(g + 3, v3);
+        pb = load_p(g + 1);
+        pv_group(pa, v0);
+        load_v(g + 4, v0);
+        pa = load_p(g + 2);
+        pv_group(pb, v1);
+        load_v(g + 5, v1);
+        pb = load_p(g + 3);
+        pv_group(pa, v2);
+        load_v(g + 6, v2);
+        pa = load_p(g + 4);
+        pv_group(pb, v3);
+      }
+      // the last ng - g < 4 groups: V already in v0, v1, v2, P of the first in pa
+      if (g < ng) {
+        pb = load_p(g + 1);
+        pv_group(pa, v0);
+      }
+      if (g + 1 < ng) {
+        pa = load_p(g + 2);
+        pv_group(pb, v1);
+      }
+      if (g + 2 < ng) pv_group(pa, v2);
     }
     // last L - Lf (< 16) keys: keys past the segment contribute exact zeros
     for (int t0 = Lf; t0 < L; t0 += 4) {
