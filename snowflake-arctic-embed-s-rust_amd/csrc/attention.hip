@@ -220,18 +220,31 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     // above the rounding error)
     const float rcols = 1.0f / (float)cols4;
     const int units = nq * cols4;
-    for (int u0 = 0; u0 < units; u0 += 256) {  // wave-uniform trip count (expf_libm needs all lanes)
-      const int u = min(u0 + tid, units - 1);
-      const int q = (int)(((float)u + 0.5f) * rcols);
-      const int c4 = u - q * cols4;
-      float* e = &S[q * pitch + 4 * c4];
-      float4 v = *reinterpret_cast<const float4*>(e);
-      const float m = s_max[q];
-      v.x = expf_libm(v.x - m, tb);
-      v.y = expf_libm(v.y - m, tb);
-      v.z = expf_libm(v.z - m, tb);
-      v.w = expf_libm(v.w - m, tb);
-      if (u0 + tid < units) *reinterpret_cast<float4*>(e) = v;
+    // two float4 units per lane and step (eight independent exps in flight);
+    // wave-uniform trip count (expf_libm needs all lanes)
+    for (int u0 = 0; u0 < units; u0 += 512) {
+      float* e[2];
+      float4 v[2];
+      float m[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const int u = min(u0 + 256 * k + tid, units - 1);
+        const int q = (int)(((float)u + 0.5f) * rcols);
+        const int c4 = u - q * cols4;
+        e[k] = &S[q * pitch + 4 * c4];
+        v[k] = *reinterpret_cast<const float4*>(e[k]);
+        m[k] = s_max[q];
+      }
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        v[k].x = expf_libm(v[k].x - m[k], tb);
+        v[k].y = expf_libm(v[k].y - m[k], tb);
+        v[k].z = expf_libm(v[k].z - m[k], tb);
+        v[k].w = expf_libm(v[k].w - m[k], tb);
+      }
+#pragma unroll
+      for (int k = 0; k < 2; k++)
+        if (u0 + 256 * k + tid < units) *reinterpret_cast<float4*>(e[k]) = v[k];
     }
   }
   __syncthreads();
@@ -241,16 +254,33 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     if (tid < nq) {
       const float* e = &S[tid * pitch];
       float sum = 0.0f;
-      int t = 0;
-      for (; t + 32 <= L; t += 32) {  // 8 loads in flight per batch of 32 sequential adds
-        float4 v[8];
+      // batches of 32 keys, each read while the previous one is added (reads past
+      // the last full batch are clamped to it and not added)
+      const int nb = L >> 5;
+      auto ld = [&](int bi, float4 (&v)[8]) {
+        const float4* src = reinterpret_cast<const float4*>(e + 32 * min(bi, nb - 1));
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = *reinterpret_cast<const float4*>(e + t + 4 * i);
+        for (int i = 0; i < 8; i++) v[i] = src[i];
+      };
+      auto add = [&](const float4 (&v)[8]) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
           sum += v[i].x; sum += v[i].y; sum += v[i].z; sum += v[i].w;
         }
+      };
+      if (nb > 0) {
+        float4 va[8], vb[8];
+        ld(0, va);
+        int bi = 0;
+        for (; bi + 2 <= nb; bi += 2) {  // va holds batch bi
+          ld(bi + 1, vb);
+          add(va);
+          ld(bi + 2, va);
+          add(vb);
+        }
+        if (bi < nb) add(va);
       }
+      int t = 32 * nb;
       for (; t + 4 <= L; t += 4) {
         const float4 v = *reinterpret_cast<const float4*>(e + t);
         sum += v.x; sum += v.y; sum += v.z; sum += v.w;
