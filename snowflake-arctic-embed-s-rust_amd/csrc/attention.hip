@@ -471,8 +471,12 @@ void init_attention_kernels() {
 // batch's mean length (both variants give the same bits).
 constexpr int kWideMinMeanLen = 48;
 
-void launch_attention(const AttnArgs& p, int T, hipStream_t st) {
+void launch_attention_plan(const AttnArgs& p, hipStream_t st) {
   hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
+}
+
+void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
+  if (plan) launch_attention_plan(p, st);
   const int max_tiles = attention_max_tiles(p.B, T);
   if (T <= 0 || p.B <= 0) return;
   const size_t lds = attention_lds_bytes(p.s_pitch);

@@ -40,6 +40,16 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // max(m, a) that ignores a NaN `a`, like `if a > max_abs { max_abs = a }`.
 __device__ __forceinline__ float nanless_max(float m, float a) { return a > m ? a : m; }
 
+// Orders this wave's LDS accesses before and after it (LDS data private to one
+// wave needs no workgroup barrier: a wave's LDS operations complete in order once
+// the counter is drained).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // bits(2^(i/32) rounded to double) - (i << 47), i = 0..31: the exp2 table of
 // expf_libm below (computed from 2^(i/32) in quad precision).
 static __constant__ uint64_t kExp2Tab[32] = {

@@ -142,6 +142,8 @@ struct ae_workspace {
   uint16_t* ids = nullptr;
   int* cu = nullptr;
   int* attn_plan = nullptr;  // attention work plan, attention_plan_ints(max_seqs, max_tokens)
+  int* splitk = nullptr;     // int32 partial sums of split-K GEMMs (small M)
+  size_t splitk_ints = 0;
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
@@ -306,6 +308,8 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.out = o;
     p.g_smooth = g_smooth;
     p.g_rowmax = g_rowmax;
+    p.partial = ws->splitk;
+    p.partial_ints = ws->splitk_ints;
     launch_gemm(p, amode, emode, st);
   };
   auto ln = [&](const float* src, float* dst, const float* gw, const float* gb, const float* smooth, int8_t* q,
@@ -354,7 +358,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
-      launch_attention(a, T, st);
+      launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
@@ -606,6 +610,10 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
       (rc = A(&ws->act_q_c, B * 384)) || (rc = A(&ws->act_scale_c, B)) || (rc = A(&ws->rowmax_ctx_c, B)) ||
       (rc = A(&ws->rowmax_g_c, B)))
     return rc;
+  // split-K partials: at most ~4.7 M int32 for any GEMM shape here once the grid
+  // is small enough to split; launch_gemm lowers the split count to fit
+  ws->splitk_ints = std::min<size_t>(size_t(6) << 20, 3 * T * 1536);
+  if ((rc = A(&ws->splitk, ws->splitk_ints))) return rc;
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_ids), T * sizeof(uint16_t), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_cu), (B + 1) * sizeof(int), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_out), B * 384 * sizeof(float), hipHostMallocDefault));

@@ -26,6 +26,8 @@
 // integer sum is exact.  Output: lane l, register r holds D[4*(l/16)+r][l%16].
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -46,16 +48,6 @@ struct ARegs {
   float4 v[4];
 };
 
-// Orders this wave's LDS accesses before and after it (LDS data private to one
-// wave needs no workgroup barrier: a wave's LDS operations complete in order once
-// the counter is drained).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // NW = columns per wave: 96 (workgroup = 384 columns, 2 waves/SIMD) or 48
 // (192 columns, 48 accumulator VGPRs: 4 waves/SIMD for int8 A, 3 for f32 A,
 // whose two-step register prefetch of A is four times larger).
@@ -72,17 +64,24 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   // row tile run back to back on one XCD and their A rows come from HBM once.
   // int8 A: row tile fastest (neighbouring workgroups share W columns and do not
   // contend on the same rows' GELU absmax atomics).
+  // Split K (p.ksplit > 1, small M): the grid repeats the items once per K range
+  // and each workgroup writes its raw int32 sums to p.partial[split][M][N];
+  // gemm_splitk_epilogue_kernel adds them (exact: integers) and applies the
+  // epilogue below.
   const int nt = p.N / kBN, mt = (p.M + kBM - 1) / kBM;
+  const int ks = p.ksplit > 1 ? p.ksplit : 1, nbase = mt * nt;
+  const int split = blockIdx.x / nbase, bid = blockIdx.x - split * nbase;
   int m0, n0;
   if constexpr (AM == kAI8) {
-    m0 = (blockIdx.x % mt) * kBM;
-    n0 = (blockIdx.x / mt) * kBN;
+    m0 = (bid % mt) * kBM;
+    n0 = (bid / mt) * kBN;
   } else {
-    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int item = ks == 1 ? xcd_contiguous(bid, nbase) : bid;
     m0 = (item / nt) * kBM;
     n0 = (item % nt) * kBN;
   }
-  const int KT = p.K >> 6;
+  const int KB = split * (p.K >> 6) / ks;            // first K step of this workgroup
+  const int KT = (split + 1) * (p.K >> 6) / ks - KB;  // K steps of this workgroup
   const int NB = p.N >> 4;  // 16-column fragments per K step in the swizzled W
   const ExpTab tb = exp_tab_regs();  // the epilogue loop below is wave-uniform
 
@@ -92,7 +91,7 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   float a_inv = 0.0f;
   if (AM != kAI8) a_inv = 127.0f / __uint_as_float(p.a_rowmax[arow]);  // inv_scale = 127.0 / max_abs
   auto aload = [&](int kt, ARegs<AM>& r) {
-    const int kb = kt * 64 + lpart * 16;
+    const int kb = (KB + kt) * 64 + lpart * 16;
     if constexpr (AM == kAI8) {
       r.v = *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(p.A) + (size_t)arow * p.K + kb);
     } else {
@@ -106,7 +105,7 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
     if constexpr (AM == kAI8) {
       q = r.v;
     } else {
-      const int kb = kt * 64 + lpart * 16;
+      const int kb = (KB + kt) * 64 + lpart * 16;
       uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -128,7 +127,7 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   auto bload = [&](int kt, v4i* dst) {
 #pragma unroll
     for (int j = 0; j < kCB; j++)
-      dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + cb0 + j) * 1024);
+      dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)(KB + kt) * NB + cb0 + j) * 1024);
   };
 
   v4i acc[4][kCB];
@@ -171,6 +170,27 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   // accumulators -> sE[16][96] (int32), then lanes walk rows with float4s
   int* E = sE[wave];
   const int col0 = n0 + wave * kWaveN;  // first column of this wave
+  if (ks > 1) {  // raw sums of this K range (uniform branch)
+    int* part = p.partial + (size_t)split * p.M * p.N;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int j = 0; j < kCB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < kF4 / 4; k++) {
+        const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
+        const int row = m0 + i * 16 + rr;
+        if (row < p.M)
+          *reinterpret_cast<int4*>(part + (size_t)row * p.N + col0 + c4 * 4) =
+              *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
+      }
+      wave_lds_sync();
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; i++) {
 #pragma unroll
@@ -220,18 +240,80 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   }
 }
 
-// int8 A: 192-column workgroups (A is small and re-read once per column tile);
-// f32 A (quantized on load): 384-column workgroups, so each A row is read once.
+// Split-K epilogue: out[row][col..col+3] from the int32 sums of the p.ksplit K
+// ranges, with the same arithmetic as gemm_w8a8_kernel's epilogue.  Block
+// (x, row) covers 256 float4 columns of one row; every lane evaluates (the
+// exact GELU needs the whole wave) and only in-range lanes write.  The GELU row
+// absmax is the max over u32 bits of the same per-float4 values the fused
+// epilogue feeds to atomicMax.
+template <int AM, int EM>
+__global__ __launch_bounds__(256) void gemm_splitk_epilogue_kernel(GemmArgs p) {
+  const ExpTab tb = exp_tab_regs();
+  const int row = blockIdx.y, n4 = p.N >> 2;
+  const int c4 = blockIdx.x * 256 + threadIdx.x;
+  const bool in = c4 < n4;
+  const int col = 4 * min(c4, n4 - 1);
+  int4 a4 = make_int4(0, 0, 0, 0);
+  for (int sp = 0; sp < p.ksplit; sp++) {
+    const int4 v = *reinterpret_cast<const int4*>(p.partial + ((size_t)sp * p.M + row) * p.N + col);
+    a4.x += v.x; a4.y += v.y; a4.z += v.z; a4.w += v.w;
+  }
+  float sa;
+  if (AM == kAI8) sa = p.a_scale[row];
+  else sa = __uint_as_float(p.a_rowmax[row]) / 127.0f;  // scale = max_abs / 127.0
+  const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
+  float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
+  if (p.res) {
+    const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)row * p.N + col);
+    b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+  }
+  float4 v;
+  v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
+  v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
+  v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
+  v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
+  if (EM == kEpiGelu) {
+    const float4 g4 = *reinterpret_cast<const float4*>(p.g_smooth + col);
+    v.x = gelu_exact(v.x, tb) * g4.x;
+    v.y = gelu_exact(v.y, tb) * g4.y;
+    v.z = gelu_exact(v.z, tb) * g4.z;
+    v.w = gelu_exact(v.w, tb) * g4.w;
+    const float gm = nanless_max(nanless_max(fabsf(v.x), fabsf(v.y)), nanless_max(fabsf(v.z), fabsf(v.w)));
+    uint32_t gb = in ? __float_as_uint(gm) : 0u;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) gb = max(gb, (uint32_t)__shfl_xor((int)gb, off, 64));
+    if ((threadIdx.x & 63) == 0 && gb != 0u) atomicMax(&p.g_rowmax[row], gb);
+  }
+  if (in) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
+}
+
+// Workgroups of 64 rows x 192 columns.  Small M (fewer than kSplitGrid
+// workgroups) splits K into ranges of at least two steps when the caller
+// provides int32 scratch (GemmArgs::partial) for the partial sums.
+constexpr int kSplitGrid = 192;
+
+template <int AM, int EM>
+static void launch_variant(GemmArgs p, hipStream_t st) {
+  const int mt = (p.M + kBM - 1) / kBM, nbase = mt * (p.N / 192), kt = p.K / 64;
+  int ks = 1;
+  if (p.partial && nbase < kSplitGrid) {
+    ks = std::min((kSplitGrid + nbase - 1) / nbase, kt / 2);
+    ks = (int)std::min<size_t>((size_t)ks, p.partial_ints / ((size_t)p.M * p.N));
+    if (ks < 2) ks = 1;
+  }
+  p.ksplit = ks;
+  hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase * ks), dim3(256), 0, st, p);
+  if (ks > 1)
+    hipLaunchKernelGGL((gemm_splitk_epilogue_kernel<AM, EM>), dim3((p.N / 4 + 255) / 256, p.M), dim3(256), 0, st,
+                       p);
+}
+
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st) {
-  const unsigned n = ((p.M + kBM - 1) / kBM) * (p.N / 192);  // 192-column workgroups
-  if (amode == kAI8 && emode == kEpiF32)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
-  else if (amode == kAI8 && emode == kEpiGelu)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<kAI8, kEpiGelu, 48>), dim3(n), dim3(256), 0, st, p);
-  else if (amode == kAF32Q && emode == kEpiF32)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32Q, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
-  else if (amode == kAF32QSmooth && emode == kEpiF32)
-    hipLaunchKernelGGL((gemm_w8a8_kernel<kAF32QSmooth, kEpiF32, 48>), dim3(n), dim3(256), 0, st, p);
+  if (p.M <= 0) return;
+  if (amode == kAI8 && emode == kEpiF32) launch_variant<kAI8, kEpiF32>(p, st);
+  else if (amode == kAI8 && emode == kEpiGelu) launch_variant<kAI8, kEpiGelu>(p, st);
+  else if (amode == kAF32Q && emode == kEpiF32) launch_variant<kAF32Q, kEpiF32>(p, st);
+  else if (amode == kAF32QSmooth && emode == kEpiF32) launch_variant<kAF32QSmooth, kEpiF32>(p, st);
 }
 
 // [N,K] row-major int8 -> [K/64][N/16][64 lanes][16 bytes]: lane l of fragment

@@ -28,6 +28,9 @@ struct GemmArgs {
   float* out;                 // [M,N]
   const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
   uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
+  int* partial;               // optional int32 scratch for split-K partial sums (small M), or null
+  size_t partial_ints;        // its capacity in int32
+  int ksplit;                 // set by launch_gemm
 };
 // N % 384 == 0, K % 64 == 0
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
@@ -80,7 +83,10 @@ inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
 // ints of `plan` scratch for B segments and T tokens: tile prefix [B+1] + tile_seg [max_tiles]
 inline size_t attention_plan_ints(int B, int T) { return (size_t)B + 1 + attention_max_tiles(B, T); }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
-void launch_attention(const AttnArgs& p, int T, hipStream_t st);  // T = total tokens of the batch
+// T = total tokens of the batch; plan = false reuses the plan already in p.plan
+// (launch_attention_plan, which depends only on cu and B)
+void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
+void launch_attention_plan(const AttnArgs& p, hipStream_t st);
 // test hook: raw results of the exact-product MFMA (16 floats per lane per set of 64 pairs)
 void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st);
 

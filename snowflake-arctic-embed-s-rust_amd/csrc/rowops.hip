@@ -21,6 +21,33 @@ namespace aek {
 constexpr int kLnRows = 32;
 constexpr int kLnPitch = 388;
 
+// Sequential sum of f(row[j]) over one 384-float LDS row (float4-aligned), in
+// index order: 12 batches of 8 float4, each read while the previous one is added.
+template <typename F>
+__device__ __forceinline__ float lds_row_sum(const float* row, F f) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  float4 va[8], vb[8];
+  auto ld = [&](int bi, float4 (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = r4[8 * min(bi, 11) + i];
+  };
+  float acc = 0.0f;
+  auto add = [&](const float4 (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      acc += f(v[i].x); acc += f(v[i].y); acc += f(v[i].z); acc += f(v[i].w);
+    }
+  };
+  ld(0, va);
+  for (int bi = 0; bi < 12; bi += 2) {
+    ld(bi + 1, vb);
+    add(va);
+    ld(bi + 2, va);
+    add(vb);
+  }
+  return acc;
+}
+
 template <int SRC>
 __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   __shared__ __attribute__((aligned(16))) float tile[kLnRows * kLnPitch];
@@ -66,22 +93,13 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   __syncthreads();
 
   if (tid < kLnRows) {
+    // sequential sums over the row, in index order
     const float* xr = &tile[tid * kLnPitch];
-    float sum = 0.0f;
-    for (int j = 0; j < H; j += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(xr + j);
-      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
-    }
-    const float mean = sum / 384.0f;
-    float var_sum = 0.0f;
-    for (int j = 0; j < H; j += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(xr + j);
-      float d;
-      d = v.x - mean; var_sum += d * d;
-      d = v.y - mean; var_sum += d * d;
-      d = v.z - mean; var_sum += d * d;
-      d = v.w - mean; var_sum += d * d;
-    }
+    const float mean = lds_row_sum(xr, [](float v) { return v; }) / 384.0f;
+    const float var_sum = lds_row_sum(xr, [mean](float v) {
+      const float d = v - mean;
+      return d * d;
+    });
     s_mean[tid] = mean;
     s_rstd[tid] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
   }
@@ -93,6 +111,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
 #pragma unroll
   for (int i = 0; i < 12; i++) {
     const int c = (sub + 8 * i) * 4;
+    xv[i] = *reinterpret_cast<const float4*>(&tile[rl * kLnPitch + c]);  // re-read: xv is dead across the sums
     const float4 g = *reinterpret_cast<const float4*>(p.gamma + c);
     const float4 b = *reinterpret_cast<const float4*>(p.beta + c);
     const float4 s = *reinterpret_cast<const float4*>(p.smooth + c);
@@ -178,37 +197,66 @@ void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, fl
   else hipLaunchKernelGGL((row_quant_kernel<false>), grid, dim3(256), 0, st, m, n, x, smooth, q, scale);
 }
 
-// final LayerNorm (no quantization, src/simd_math.rs:481-497) and L2 normalize
-// (src/simd_math.rs:2892-2903), one lane per row, sequential sums
-__global__ __launch_bounds__(64) void final_ln_l2_kernel(int B, const float* src, const float* gamma,
-                                                         const float* beta, float* out) {
-  const int b = blockIdx.x * 64 + threadIdx.x;
-  if (b >= B) return;
-  const float* x = src + (size_t)b * H;
-  float* y = out + (size_t)b * H;
-  float sum = 0.0f;
-  for (int j = 0; j < H; j++) sum += x[j];
-  const float mean = sum / 384.0f;
-  float var_sum = 0.0f;
-  for (int j = 0; j < H; j++) {
-    const float d = x[j] - mean;
-    var_sum += d * d;
+// final LayerNorm (no quant) then L2 normalize of the B [CLS] rows
+// (layernorm_inplace_row + l2_normalize_inplace, src/simd_math.rs:481-497,
+// :2892-2903): one wave per row.  The row sits in LDS; lane 0 takes the three
+// sequential sums (mean, variance, sum of squares) in index order, all lanes
+// the elementwise steps.
+__global__ __launch_bounds__(256) void final_ln_l2_kernel(int B, const float* src, const float* gamma,
+                                                          const float* beta, float* out) {
+  __shared__ __attribute__((aligned(16))) float tile[4][kLnPitch];
+  __shared__ float s_stat[4][2];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + wave;
+  if (b >= B) return;  // wave-uniform; the waves below synchronize only with themselves
+  float* t = tile[wave];
+  const float4* x4 = reinterpret_cast<const float4*>(src + (size_t)b * H);
+  // float4 columns of this lane: lane, and 64 + lane for lane < 32
+  const bool two = lane < 32;
+  float4 xa = x4[lane], xb = two ? x4[64 + lane] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  reinterpret_cast<float4*>(t)[lane] = xa;
+  if (two) reinterpret_cast<float4*>(t)[64 + lane] = xb;
+  wave_lds_sync();
+  if (lane == 0) {
+    const float mean = lds_row_sum(t, [](float v) { return v; }) / 384.0f;
+    const float var_sum = lds_row_sum(t, [mean](float v) {
+      const float d = v - mean;
+      return d * d;
+    });
+    s_stat[wave][0] = mean;
+    s_stat[wave][1] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
   }
-  const float rstd = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
-  float sum_sq = 0.0f;
-  for (int j = 0; j < H; j++) {
-    const float v = (x[j] - mean) * rstd * gamma[j] + beta[j];
-    y[j] = v;
-    sum_sq += v * v;
-  }
+  wave_lds_sync();
+  const float mean = s_stat[wave][0], rstd = s_stat[wave][1];
+  auto ln4 = [&](float4 v, int c4) {
+    const float4 g = reinterpret_cast<const float4*>(gamma)[c4];
+    const float4 be = reinterpret_cast<const float4*>(beta)[c4];
+    v.x = (v.x - mean) * rstd * g.x + be.x;
+    v.y = (v.y - mean) * rstd * g.y + be.y;
+    v.z = (v.z - mean) * rstd * g.z + be.z;
+    v.w = (v.w - mean) * rstd * g.w + be.w;
+    return v;
+  };
+  xa = ln4(xa, lane);
+  if (two) xb = ln4(xb, 64 + lane);
+  reinterpret_cast<float4*>(t)[lane] = xa;
+  if (two) reinterpret_cast<float4*>(t)[64 + lane] = xb;
+  wave_lds_sync();
+  if (lane == 0) s_stat[wave][0] = lds_row_sum(t, [](float v) { return v * v; });
+  wave_lds_sync();
+  const float sum_sq = s_stat[wave][0];
+  float4* y4 = reinterpret_cast<float4*>(out + (size_t)b * H);
   if (sum_sq > 0.0f) {
     const float inv_norm = 1.0f / sqrtf(sum_sq);
-    for (int j = 0; j < H; j++) y[j] = y[j] * inv_norm;
+    xa.x = xa.x * inv_norm; xa.y = xa.y * inv_norm; xa.z = xa.z * inv_norm; xa.w = xa.w * inv_norm;
+    xb.x = xb.x * inv_norm; xb.y = xb.y * inv_norm; xb.z = xb.z * inv_norm; xb.w = xb.w * inv_norm;
   }
+  y4[lane] = xa;
+  if (two) y4[64 + lane] = xb;
 }
 
 void launch_final_ln_l2(int B, const float* src, const float* gamma, const float* beta, float* out, hipStream_t st) {
-  hipLaunchKernelGGL(final_ln_l2_kernel, dim3((B + 63) / 64), dim3(64), 0, st, B, src, gamma, beta, out);
+  if (B > 0) hipLaunchKernelGGL(final_ln_l2_kernel, dim3((B + 3) / 4), dim3(256), 0, st, B, src, gamma, beta, out);
 }
 
 // fills a u32 buffer (row-absmax initial values, bits of 1e-8f)
