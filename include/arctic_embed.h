@@ -152,7 +152,8 @@ int ae_gelu_smooth_quantize(int m, int n, float* x_dev, const float* inv_smooth_
                             float* scale_dev, void* stream);
 /* Segment-bounded multi-head attention of one layer (src/model.rs:663-694):
  * qkv_dev [T,1152] f32 (Q|K|V, head h at column h*32), cu_seqlens_dev [n_seqs+1],
- * ctx_dev [T,384] f32. */
+ * ctx_dev [T,384] f32.  Synchronous: reads cu_seqlens back to size the work;
+ * segments longer than 512 are cut to their first 512 rows. */
 int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
                         int total_tokens, float* ctx_dev, void* stream);
 

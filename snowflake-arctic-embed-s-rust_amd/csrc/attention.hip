@@ -436,6 +436,145 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   }
 }
 
+// Short rows (every sequence of the batch at most 16 * NKB <= 64 keys): one
+// workgroup per (sequence, head), one wave per 16 queries, the whole score row
+// in registers (NKB blocks of 16 keys, 4 scores per lane and block), no LDS tile
+// and no barrier.  Same arithmetic, in the same order, as attention_kernel:
+//  * scores: A = K block with its rows permuted so that lane (lg, lr) ends with
+//    query lr and keys 16kb + lg + 4i in result register i, B = Q (dims 4j + b);
+//  * the in-order denominator: each lane gathers the 16 exps of its query and
+//    block (key 16kb + lg' + 4i from lane lr + 16lg', register i) and adds them
+//    in key order (padding keys hold exact +0);
+//  * PV: MFMA i of block kb multiplies keys 16kb + 4i + j (block j), so register
+//    i is directly its A operand; lane (lg, lr) ends with queries 4lg + r at
+//    dims lr and 16 + lr.
+// Batches of short sequences spend most of a tiled workgroup on set-up and
+// partial tiles; this form keeps 6 waves per SIMD busy instead.
+template <int NKB>
+__global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
+  const int item = xcd_contiguous(blockIdx.x, p.B * 12);
+  const int h = item / p.B, b = item - h * p.B;
+  const int s0 = p.cu[b];
+  const int L = min(p.cu[b + 1] - s0, 16 * NKB);
+  const int lane = threadIdx.x & 63, q0 = (threadIdx.x >> 6) * 16;
+  if (q0 >= L) return;  // wave-uniform; nothing below synchronizes across waves
+  const int lr = lane & 15, lg = lane >> 4;
+  const ExpTab tb = exp_tab_regs();
+  const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
+  const int nkb = (L + 15) >> 4;
+
+  float qf[8];
+  {
+    const float* qrow = qkv + (size_t)min(q0 + lr, L - 1) * HQKV;
+#pragma unroll
+    for (int j = 0; j < 8; j++) qf[j] = qrow[4 * j + lg];
+  }
+  const int kperm = 4 * (lr & 3) + (lr >> 2);  // key of A row lr within a block
+  auto load_kf = [&](int kb, float (&kf)[8]) {
+    const float* src = qkv + H + lg + (size_t)min(16 * kb + kperm, L - 1) * HQKV;
+#pragma unroll
+    for (int j = 0; j < 8; j++) kf[j] = src[4 * j];
+  };
+  float s[NKB][4];
+  float mx = -INFINITY;
+  {
+    float kf[2][8];
+    load_kf(0, kf[0]);
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+      if (kb < nkb) {  // wave-uniform
+        if (kb + 1 < nkb) load_kf(kb + 1, kf[(kb + 1) & 1]);
+        float acc[4];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const v16f pr = mfma_products(kf[kb & 1][j], qf[j]);
+#pragma unroll
+          for (int blk = 0; blk < 4; blk++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)  // starts from the first product (a zero sum's sign cannot matter)
+              acc[i] = (j == 0 && blk == 0) ? pr[i] : acc[i] + pr[4 * blk + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          s[kb][i] = acc[i] * kInvSqrtD;
+          if (16 * kb + lg + 4 * i < L) mx = fmaxf(mx, s[kb][i]);
+        }
+      }
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+
+  float sum = 0.0f;
+#pragma unroll
+  for (int kb = 0; kb < NKB; kb++) {
+    if (kb < nkb) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float e = expf_libm(s[kb][i] - mx, tb);
+        s[kb][i] = (16 * kb + lg + 4 * i < L) ? e : 0.0f;
+      }
+      float v[16];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) v[g + 4 * i] = __shfl(s[kb][i], lr + 16 * g, 64);
+#pragma unroll
+      for (int t = 0; t < 16; t++) sum += v[t];
+    }
+  }
+  const float inv = 1.0f / sum;
+
+  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  auto load_vf = [&](int kb, float (&vf)[2][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float* src = qkv + 2 * H + lr + (size_t)min(16 * kb + 4 * i + lg, L - 1) * HQKV;
+      vf[0][i] = src[0];
+      vf[1][i] = src[16];
+    }
+  };
+  {
+    float vf[2][2][4];
+    load_vf(0, vf[0]);
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb++) {
+      if (kb < nkb) {
+        if (kb + 1 < nkb) load_vf(kb + 1, vf[(kb + 1) & 1]);
+        if (kb + 1 == nkb) {  // keys past the segment: exact zeros
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (16 * kb + 4 * i + lg >= L) vf[kb & 1][0][i] = vf[kb & 1][1][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float pi = s[kb][i] * inv;
+          add_blocks(acc[0], mfma_products(pi, vf[kb & 1][0][i]));
+          add_blocks(acc[1], mfma_products(pi, vf[kb & 1][1][i]));
+        }
+      }
+    }
+  }
+  const float sm0 = p.rowmax ? p.smooth[h * 32 + lr] : 0.0f;
+  const float sm1 = p.rowmax ? p.smooth[h * 32 + 16 + lr] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int q = q0 + 4 * lg + r;
+    if (q < L) {
+      float* o = p.ctx + (size_t)(s0 + q) * H + h * 32 + lr;
+      o[0] = acc[0][r];
+      o[16] = acc[1][r];
+    }
+    if (p.rowmax) {
+      float a = nanless_max(0.0f, fabsf(acc[0][r] * sm0));
+      a = nanless_max(a, fabsf(acc[1][r] * sm1));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
+      if (q < L && lr == 0) atomicMax(&p.rowmax[s0 + q], __float_as_uint(a));
+    }
+  }
+}
+
 // test hook: for each set of 64 operand pairs, the 16 results per lane of
 // mfma_products (out[set][lane][r]), the multiplier attention_kernel relies on
 __global__ __launch_bounds__(64) void mfma_products_kernel(const float* a, const float* b, float* out, int n_sets) {
@@ -476,9 +615,18 @@ void launch_attention_plan(const AttnArgs& p, hipStream_t st) {
 }
 
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
+  if (T <= 0 || p.B <= 0) return;
+  const int max_len = p.s_pitch - 4;  // round16 of the longest sequence
+  if (max_len <= 32) {
+    hipLaunchKernelGGL(attention_rows_kernel<2>, dim3(p.B * 12), dim3(256), 0, st, p);
+    return;
+  }
+  if (max_len <= 64) {
+    hipLaunchKernelGGL(attention_rows_kernel<4>, dim3(p.B * 12), dim3(256), 0, st, p);
+    return;
+  }
   if (plan) launch_attention_plan(p, st);
   const int max_tiles = attention_max_tiles(p.B, T);
-  if (T <= 0 || p.B <= 0) return;
   const size_t lds = attention_lds_bytes(p.s_pitch);
   if (T > kWideMinMeanLen * p.B)
     hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);

@@ -778,11 +778,22 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   if (!qkv_dev || !cu_seqlens_dev || !ctx_dev || n_seqs < 0 || total_tokens < 0)
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
   if (n_seqs == 0) return AE_OK;
+  // the longest segment sizes the score rows and picks the kernel variant
+  std::vector<int32_t> cu(size_t(n_seqs) + 1);
+  HIP_TRY(hipMemcpyAsync(cu.data(), cu_seqlens_dev, cu.size() * sizeof(int32_t), hipMemcpyDeviceToHost,
+                         as_stream(stream)));
+  HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+  int max_len = 1;
+  for (int b = 0; b < n_seqs; b++) {
+    const int L = cu[b + 1] - cu[b];
+    if (L < 0 || cu[b + 1] > total_tokens) return fail(AE_ERR_INVALID_ARG, "cu_seqlens is not a prefix sum of total_tokens");
+    max_len = std::max(max_len, L);
+  }
   int* plan = nullptr;
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs, total_tokens) * sizeof(int)));
   aek::init_attention_kernels();
   aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
-                  aek::attention_pitch(ae::kMaxPos)};
+                  aek::attention_pitch(std::min(max_len, ae::kMaxPos))};
   aek::launch_attention(a, total_tokens, as_stream(stream));
   hipError_t err = hipStreamSynchronize(as_stream(stream));
   (void)hipFree(plan);

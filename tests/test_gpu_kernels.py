@@ -183,10 +183,13 @@ def test_gelu_bit_exact_over_float_sample(torch_gpu):
     assert np.array_equal(bits(y)[~nan], bits(ref)[~nan])
 
 
-# the attention kernel has two operand layouts, chosen by the batch's mean length
-# (48): these length sets reach both
-ATTN_LENS = {"mean81": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
-             "mean17": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8]}
+# attention has four code paths, chosen by the batch's longest and mean lengths:
+# register-resident rows (longest <= 32, <= 64), else the tiled kernel with the
+# wide (mean > 48) or the narrow operand layout; these length sets reach each
+ATTN_LENS = {"tiled_wide": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
+             "tiled_narrow": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 100],
+             "rows64": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 64],
+             "rows32": [1, 2, 17, 31, 32, 3, 9, 16, 15, 8]}
 
 
 @pytest.mark.parametrize("lens", list(ATTN_LENS.values()), ids=list(ATTN_LENS))
@@ -236,7 +239,8 @@ def test_mfma_products_equal_rounded_products(torch_gpu):
     assert np.count_nonzero((ref != 0) & (np.abs(ref) < np.finfo(f32).tiny)) > 1000  # denormals were covered
 
 
-@pytest.mark.parametrize("lens", [[5, 40, 97, 300], [5, 40, 19, 33, 1]], ids=["mean110", "mean20"])
+@pytest.mark.parametrize("lens", [[5, 40, 97, 300], [5, 40, 19, 33, 1, 90], [5, 40, 19, 33, 1], [5, 31, 19, 27, 1]],
+                         ids=["tiled_wide", "tiled_narrow", "rows64", "rows32"])
 def test_attention_bit_exact_extreme_magnitudes(torch_gpu, lens):
     """Scores and PV terms with denormal products, exact zeros and huge dynamic range."""
     torch = torch_gpu
