@@ -29,13 +29,15 @@ constexpr int kAttnQ = 32;     // queries per workgroup
 // Work plan, built on the device from cu_seqlens: plan[b] = sum_{b'<b}
 // ceil(L_b'/kAttnQ) (plan[B] = number of tiles) and, after it, tile_seg[tile] =
 // the segment of each tile, so a workgroup finds its segment with one load.
-__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int* plan) {
+// Tiles follow the packed segment order (neighbouring tiles read neighbouring
+// K/V rows).  Rows past lmax (the score row length) get no tiles.
+__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int* plan) {
   __shared__ int part[256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
   int nt = 0;
-  for (int b = b0; b < b1; b++) nt += (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
+  for (int b = b0; b < b1; b++) nt += (min(cu[b + 1] - cu[b], lmax) + kAttnQ - 1) / kAttnQ;
   part[tid] = nt;
   __syncthreads();
   if (tid == 0) {
@@ -52,7 +54,7 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
   int at = part[tid];
   for (int b = b0; b < b1; b++) {
     plan[b] = at;
-    const int n = (cu[b + 1] - cu[b] + kAttnQ - 1) / kAttnQ;
+    const int n = (min(cu[b + 1] - cu[b], lmax) + kAttnQ - 1) / kAttnQ;
     for (int i = 0; i < n; i++) tile_seg[at + i] = b;
     at += n;
   }
@@ -611,7 +613,7 @@ void init_attention_kernels() {
 constexpr int kWideMinMeanLen = 48;
 
 void launch_attention_plan(const AttnArgs& p, hipStream_t st) {
-  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.plan);
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4, p.plan);
 }
 
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
