@@ -31,6 +31,7 @@ struct GemmArgs {
   int* partial;               // optional int32 scratch for split-K partial sums (small M), or null
   size_t partial_ints;        // its capacity in int32
   int ksplit;                 // set by launch_gemm
+  int col_fast;               // set by launch_gemm: workgroup order (column tile fastest)
 };
 // N % 384 == 0, K % 64 == 0
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
