@@ -48,10 +48,22 @@ __device__ __forceinline__ float lds_row_sum(const float* row, F f) {
   return acc;
 }
 
-template <int SRC>
+// LAT (few rows: latency, not bandwidth, bounds the launch): gamma, beta and
+// inv_smooth are loaded into registers at the start instead of after the sums.
+template <int SRC, bool LAT>
 __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   __shared__ __attribute__((aligned(16))) float tile[kLnRows * kLnPitch];
   __shared__ float s_mean[kLnRows], s_rstd[kLnRows];
+  float4 pg[LAT ? 12 : 1], pb[LAT ? 12 : 1], ps[LAT ? 12 : 1];
+  if constexpr (LAT) {
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = ((threadIdx.x & 7) + 8 * i) * 4;
+      pg[i] = *reinterpret_cast<const float4*>(p.gamma + c);
+      pb[i] = *reinterpret_cast<const float4*>(p.beta + c);
+      ps[i] = *reinterpret_cast<const float4*>(p.smooth + c);
+    }
+  }
   const int tid = threadIdx.x, rl = tid >> 3, sub = tid & 7;
   const int row = blockIdx.x * kLnRows + rl;
   const bool valid = row < p.T;
@@ -112,9 +124,9 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   for (int i = 0; i < 12; i++) {
     const int c = (sub + 8 * i) * 4;
     xv[i] = *reinterpret_cast<const float4*>(&tile[rl * kLnPitch + c]);  // re-read: xv is dead across the sums
-    const float4 g = *reinterpret_cast<const float4*>(p.gamma + c);
-    const float4 b = *reinterpret_cast<const float4*>(p.beta + c);
-    const float4 s = *reinterpret_cast<const float4*>(p.smooth + c);
+    const float4 g = LAT ? pg[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.gamma + c);
+    const float4 b = LAT ? pb[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.beta + c);
+    const float4 s = LAT ? ps[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.smooth + c);
     float4 y;
     y.x = (xv[i].x - mean) * rstd * g.x + b.x;
     y.y = (xv[i].y - mean) * rstd * g.y + b.y;
@@ -147,10 +159,20 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   }
 }
 
+// up to this many workgroups (a small fraction of the GPU) the launch is
+// latency-bound and takes the LAT variant
+constexpr int kLnLatencyGrid = 64;
+
 void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st) {
-  dim3 grid((p.T + kLnRows - 1) / kLnRows);
-  if (src_mode == kLnSrcEmb) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb>), grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32>), grid, dim3(256), 0, st, p);
+  const int n = (p.T + kLnRows - 1) / kLnRows;
+  const bool lat = n <= kLnLatencyGrid;
+  if (src_mode == kLnSrcEmb) {
+    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, true>), dim3(n), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, false>), dim3(n), dim3(256), 0, st, p);
+  } else {
+    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, true>), dim3(n), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, false>), dim3(n), dim3(256), 0, st, p);
+  }
 }
 
 // ---------------------------------------------------------------------------
