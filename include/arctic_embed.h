@@ -172,8 +172,8 @@ int ae_write_synthetic_ae8(const char* path, uint64_t seed);
 #define AE_KERNEL_ATTENTION 2
 #define AE_KERNEL_GEMM_ATTN_OUT 3
 #define AE_KERNEL_LN1 4
-#define AE_KERNEL_GEMM_FFN_UP 5
-#define AE_KERNEL_GEMM_FFN_DOWN 6
+#define AE_KERNEL_GEMM_FFN_UP 5 /* the whole fused FFN block when a pass has >= 4096 tokens */
+#define AE_KERNEL_GEMM_FFN_DOWN 6 /* unused (count 0) when the FFN block is fused */
 #define AE_KERNEL_LN2 7
 #define AE_KERNEL_LAYER11_TAIL 8
 #define AE_KERNEL_KINDS 9
@@ -192,6 +192,13 @@ int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const u
  * rowmax[m] = max(rowmax[m], max_n |g|) on f32 bits (caller pre-sets rowmax). */
 int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
                        const float* g_smooth_dev, float* out_dev, uint32_t* rowmax_dev, void* stream);
+/* The FFN block of src/model.rs:725-755 as the forward pass runs it at large
+ * token counts (one kernel, no [m,1536] intermediate in memory):
+ * out = gemm_int8_fused(ffn_out, gelu_smooth_quantize(gemm_int8_fused(ffn_inter, a)), res).
+ * up: 384 -> 1536 linear, down: 1536 -> 384 linear (its inv_smooth smooths the
+ * GELU output).  out may equal res. */
+int ae_debug_ffn(const ae_linear* up, const ae_linear* down, int m, const int8_t* a_dev, const float* a_scale_dev,
+                 const float* res_dev, float* out_dev, void* stream);
 /* Embedding + the first `layers` (0..11) encoder layers over one packed batch of n
  * sequences (given order, each 1..512 ids); copies back hidden [T,384] f32,
  * act_q [T,384] int8 and act_scale [T] (T = offsets[n]), the state that

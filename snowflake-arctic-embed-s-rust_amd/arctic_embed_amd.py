@@ -78,6 +78,7 @@ _SIGS = {
     "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
     "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_gemm_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ae_debug_ffn": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -334,6 +335,11 @@ class Linear:
     def gemm_gelu(self, m, a_ptr, a_scale_ptr, g_smooth_ptr, out_ptr, rowmax_ptr, stream=None):
         """GEMM with the GELU * smooth epilogue and row absmax (the FFN-up variant)."""
         _check(_lib.ae_debug_gemm_gelu(self._h, int(m), a_ptr, a_scale_ptr, g_smooth_ptr, out_ptr, rowmax_ptr, stream))
+
+    def ffn(self, down, m, a_ptr, a_scale_ptr, res_ptr, out_ptr, stream=None):
+        """The fused FFN block (src/model.rs:725-755) with this linear as FFN-up
+        (384 -> 1536) and `down` as FFN-down (1536 -> 384); out may equal res."""
+        _check(_lib.ae_debug_ffn(self._h, down._h, int(m), a_ptr, a_scale_ptr, res_ptr, out_ptr, stream))
 
     def close(self):
         if self._h:

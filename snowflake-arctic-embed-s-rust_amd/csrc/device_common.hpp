@@ -32,6 +32,21 @@ __device__ __forceinline__ int qround(float v) {
   return (int)r;
 }
 
+// qround for |x| <= 127.5 or NaN, which holds wherever x = v * (127 / max_abs)
+// with max_abs >= |v| (|x| <= 127 * (1 + 2^-24)^2 after the two roundings):
+// round half away from zero as trunc(|x| + (0.5 - 2^-25)) with x's sign.  That
+// sum rounds up to the next integer exactly when |x| has a fraction >= 0.5: equal
+// to roundf on all 1.12 G non-negative floats up to 127.5 (exhaustive CPU check).
+// The clamp to [-127, 127] cannot bind in that range; v_cvt_i32_f32 maps NaN to
+// 0, as the reference's `as i8` does (inline asm: a C++ float-to-int cast of NaN
+// would be undefined).
+__device__ __forceinline__ int qround_bounded(float x) {
+  const float r = copysignf(__builtin_truncf(fabsf(x) + 0x1.fffffep-2f), x);
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+  return q;
+}
+
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
          ((uint32_t)(d & 0xff) << 24);
@@ -116,9 +131,18 @@ __device__ __forceinline__ float expf_libm(float x, const ExpTab& tb) {
 
 // scalar_gelu (reference src/simd_math.rs:15-23), same operation order.
 // Wave-uniform control flow required (see ExpTab).
+//
+// t = 1 / (1 + p z) is v_rcp_f32 plus one Newton step instead of the IEEE
+// divide sequence: on every float y in [1, 8) the two are bit-identical
+// (all 25.2 M values compared on gfx950).  y is clamped at 8 first: there
+// z >= 21.3, exp(-z^2) is +0, and erf is +-1 whatever finite t is, so the clamp
+// changes nothing and keeps t finite for x = +-inf.  The whole function equals
+// the IEEE-divide form on all 2^32 inputs (NaN for NaN), at ~10 % fewer cycles.
 __device__ __forceinline__ float gelu_exact(float x, const ExpTab& tb) {
   const float z = fabsf(x) * 0.70710677f;
-  const float t = 1.0f / (1.0f + 0.3275911f * z);
+  const float y = fminf(1.0f + 0.3275911f * z, 8.0f);
+  const float r0 = __builtin_amdgcn_rcpf(y);
+  const float t = __builtin_fmaf(__builtin_fmaf(-y, r0, 1.0f), r0, r0);
   const float poly =
       t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
   const float erf_val = copysignf(1.0f - poly * expf_libm(-z * z, tb), x);

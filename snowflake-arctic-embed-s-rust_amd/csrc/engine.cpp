@@ -275,6 +275,29 @@ struct KernelTimer {
   }
 };
 
+// The FFN block runs as one fused kernel (aek::launch_ffn) from this many token
+// rows on: its workgroups own 32 whole rows, one per CU, so below a few
+// thousand rows the split-K GEMM pair keeps more of the GPU busy.
+constexpr int kFfnFusedMinRows = 4096;
+
+static aek::FfnArgs ffn_args(const ae_linear& up, const ae_linear& down, int m, const int8_t* a, const float* a_scale,
+                             const float* res, float* out) {
+  aek::FfnArgs f{};
+  f.M = m;
+  f.A = a;
+  f.a_scale = a_scale;
+  f.w1 = up.w;
+  f.w1_scale = up.w_scale;
+  f.b1 = up.bias;
+  f.g_smooth = down.inv_smooth;
+  f.w2 = down.w;
+  f.w2_scale = down.w_scale;
+  f.b2 = down.bias;
+  f.res = res;
+  f.out = out;
+  return f;
+}
+
 // one forward pass over a token-packed batch already resident on the device
 // (PackedModel::forward_ragged_cls, src/model.rs:521-914, without its 64-sequence /
 // 512-token limits).  ids/cu may be the workspace's or the caller's buffers;
@@ -369,15 +392,20 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       KernelTimer kt(ws, st, AE_KERNEL_LN1);
       ln(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale, ws->rowmax_g, T);
     }
-    {
+    if (T >= kFfnFusedMinRows) {  // FFN-up, GELU, quantize and FFN-down in one kernel
       KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
-      gemm(D.ffn_inter, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->g, kEpiGelu,
-           D.ffn_out.inv_smooth, ws->rowmax_g);
-    }
-    {
-      KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
-      gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
-           nullptr);
+      launch_ffn(ffn_args(D.ffn_inter, D.ffn_out, T, ws->act_q, ws->act_scale, ws->hidden, ws->tmp), st);
+    } else {
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
+        gemm(D.ffn_inter, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->g, kEpiGelu,
+             D.ffn_out.inv_smooth, ws->rowmax_g);
+      }
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
+        gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
+             nullptr);
+      }
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_LN2);
@@ -907,6 +935,17 @@ int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const flo
   p.g_smooth = g_smooth_dev;
   p.g_rowmax = rowmax_dev;
   aek::launch_gemm(p, aek::kAI8, aek::kEpiGelu, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_debug_ffn(const ae_linear* up, const ae_linear* down, int m, const int8_t* a_dev, const float* a_scale_dev,
+                 const float* res_dev, float* out_dev, void* stream) {
+  if (!up || !down || m <= 0 || !a_dev || !a_scale_dev || !res_dev || !out_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad arguments");
+  if (up->k != ae::kHidden || up->n != ae::kInter || down->k != ae::kInter || down->n != ae::kHidden)
+    return fail(AE_ERR_INVALID_ARG, "ffn: expects a 384->1536 and a 1536->384 linear");
+  aek::launch_ffn(ffn_args(*up, *down, m, a_dev, a_scale_dev, res_dev, out_dev), as_stream(stream));
   HIP_TRY(hipGetLastError());
   return AE_OK;
 }

@@ -1,0 +1,262 @@
+// ffn.hip -- the FFN block of one encoder layer as one gfx950 kernel:
+//
+//   g   = GELU(fma(f32(A . W1^T), sa*ws1, b1)) * inv_smooth2      FFN-up + GELU
+//   q,s = per-row absmax int8 quantization of g                    gelu_smooth_quantize
+//   out = fma(f32(q . W2^T), s*ws2, b2 + res)                       FFN-down + residual
+//
+// (reference src/model.rs:725-755: gemm_int8_fused(ffn_inter) -> inter_buf,
+// gelu_smooth_quantize_batch -> inter_q/act_scale, gemm_int8_fused(ffn_out,
+// residual hidden); the arithmetic of each step is the one of gemm.hip's
+// kEpiGelu epilogue, the row quantizer and the kAF32Q epilogue.)
+//
+// One workgroup (8 waves) owns 32 complete token rows.  The row absmax of g is
+// therefore known inside the workgroup, and the [rows, 1536] intermediate never
+// leaves the CU: the GELU values overwrite the FFN-up accumulator registers in
+// place, their int8 quantization is written to LDS, and that LDS tile is the A
+// operand of the FFN-down MFMAs.  Compared with two GEMMs this removes the f32
+// intermediate's HBM round trip (12 bytes per element: f32 write, f32 read at
+// quantize-on-load) and the second GEMM's A-quantization work.
+//
+// Wave w computes FFN-up columns [192w, 192w+192) for all 32 rows (2 x 12 tiles
+// of v_mfma_i32_16x16x64_i8, 96 accumulator VGPRs) and FFN-down columns
+// [48w, 48w+48) (2 x 3 tiles).  Weights are the pre-swizzled fragment order of
+// gemm.hip ([K/64][N/16][64 lanes][16 B]), streamed per wave from L2.
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aek {
+
+namespace {
+constexpr int kH = 384, kF = 1536;
+constexpr int kRows = 32;                 // token rows per workgroup
+constexpr int kWaves = 8;
+constexpr int kAPitch = kH + 16;          // LDS row pitch of the input tile (bytes)
+constexpr int kQPitch = kF + 16;          // LDS row pitch of the quantized intermediate (bytes)
+constexpr int kUpCB = kF / 16 / kWaves;   // FFN-up 16-column blocks per wave (12)
+constexpr int kDnCB = kH / 16 / kWaves;   // FFN-down 16-column blocks per wave (3)
+constexpr int kEPitch = kDnCB * 16 + 4;   // per-wave epilogue staging row pitch (words)
+constexpr int kRing = 8;                  // FFN-down K steps of weight fragments in flight
+constexpr int kUpSteps = kH / 64, kDnSteps = kF / 64;
+
+// DPP lane permutations within rows of 16 lanes
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xF, 0xF, true);  // every lane has a source
+}
+
+// max over the 16 lanes of this lane's DPP row (every lane gets it)
+__device__ __forceinline__ float row16_max(float m) {
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor1>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor2>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(m))));
+  return fmaxf(m, __uint_as_float(dpp<kDppMirror>(__float_as_uint(m))));
+}
+
+// 4 x 4 byte transpose over the lanes of a quad: lane k holds byte r = M[r][k]
+// (a column); afterwards it holds byte c = M[k][c] (a row).  Two exchanges
+// (lane k^1, then k^2), each followed by one byte select (v_perm_b32: selector
+// values 0-3 pick bytes of the second operand, 4-7 of the first).
+__device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t v, int k) {
+  const uint32_t w = __builtin_amdgcn_perm(dpp<kDppXor1>(v), v, (k & 1) ? 0x03070105u : 0x06020400u);
+  return __builtin_amdgcn_perm(dpp<kDppXor2>(w), w, (k & 2) ? 0x03020706u : 0x05040100u);
+}
+}  // namespace
+
+__global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
+  __shared__ __attribute__((aligned(16))) int8_t sA[kRows * kAPitch];
+  __shared__ __attribute__((aligned(16))) int8_t sQ[kRows * kQPitch];
+  __shared__ __attribute__((aligned(16))) float sMax[kRows][kWaves];  // per-wave row absmax of g
+  __shared__ __attribute__((aligned(16))) int sE[kWaves][kRows * kEPitch];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fq = lane >> 4;  // MFMA: operand row / output column; k group / output row quad
+  const int m0 = blockIdx.x * kRows;
+
+  // input tile: 32 rows x 384 int8 (rows past M repeat row M-1; never stored)
+  for (int c = tid; c < kRows * (kH / 16); c += 512) {
+    const int row = c / (kH / 16), c16 = c - row * (kH / 16);
+    const int grow = min(m0 + row, p.M - 1);
+    *reinterpret_cast<v4i*>(&sA[row * kAPitch + c16 * 16]) =
+        __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.A + (size_t)grow * kH + c16 * 16));
+  }
+
+  // ---- FFN-up: acc[i][j] = rows 16i.., columns (12w + j)*16.. ----
+  const int cb1 = wave * kUpCB;
+  const int8_t* w1 = p.w1 + (size_t)lane * 16;
+  auto load_b1 = [&](int kt, v4i* dst) {
+#pragma unroll
+    for (int j = 0; j < kUpCB; j++)
+      dst[j] = *reinterpret_cast<const v4i*>(w1 + ((size_t)kt * (kF / 16) + cb1 + j) * 1024);
+  };
+  v4i b1[2][kUpCB];
+  load_b1(0, b1[0]);
+  __syncthreads();
+  v4i acc[2][kUpCB];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < kUpCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int kt = 0; kt < kUpSteps; kt++) {  // fully unrolled: the two fragment buffers alternate without copies
+    if (kt + 1 < kUpSteps) load_b1(kt + 1, b1[(kt + 1) & 1]);
+    v4i af[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAPitch + kt * 64 + fq * 16]);
+#pragma unroll
+    for (int j = 0; j < kUpCB; j++)
+#pragma unroll
+      for (int i = 0; i < 2; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], b1[kt & 1][j], acc[i][j], 0, 0, 0);
+  }
+
+  // ---- epilogue of FFN-up: g = GELU(fma(f32(acc), sa*ws, b)) * inv_smooth, in place ----
+  // This lane holds rows 16i + 4fq + r (i < 2, r < 4) of column (cb1 + j)*16 + fr.
+  float sa[2][4], mx[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      sa[i][r] = p.a_scale[min(m0 + i * 16 + fq * 4 + r, p.M - 1)];
+      mx[i][r] = 1e-8f;  // max_abs starts at 1e-8 (src/simd_math.rs:1295-1312)
+    }
+  const ExpTab tb = exp_tab_regs();  // wave-uniform from here to the end of the loop
+#pragma unroll
+  for (int j = 0; j < kUpCB; j++) {
+    const int col = (cb1 + j) * 16 + fr;
+    const float ws = p.w1_scale[col], bb = p.b1[col], gs = p.g_smooth[col];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float v = fmaf((float)acc[i][j][r], sa[i][r] * ws, bb);
+        float g = gelu_exact(v, tb) * gs;
+        // g is materialized here, in program order: without this the compiler
+        // sinks the GELU tails towards their later uses and keeps every
+        // head's double-precision temporaries live (hundreds of spills)
+        asm volatile("" : "+v"(g));
+        acc[i][j][r] = __float_as_int(g);
+        mx[i][r] = nanless_max(mx[i][r], fabsf(g));
+      }
+  }
+  // row absmax: over the 16 lanes of this row quad (no NaN: nanless_max above),
+  // then over the 8 waves via LDS
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) mx[i][r] = row16_max(mx[i][r]);
+  if (fr == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) sMax[i * 16 + fq * 4 + r][wave] = mx[i][r];
+  }
+  __syncthreads();
+  auto row_absmax = [&](int row) {
+    const float4 a = *reinterpret_cast<const float4*>(&sMax[row][0]);
+    const float4 b = *reinterpret_cast<const float4*>(&sMax[row][4]);
+    return fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w)));
+  };
+
+  // ---- quantize: q = round(g * (127 / max_abs)) into the LDS tile ----
+  // A lane's 4 values of one tile are 4 rows of one column; a quad byte
+  // transpose turns them into 4 columns of one row, written as one dword.
+  const int qk = fr & 3;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    float inv_scale[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) inv_scale[r] = 127.0f / row_absmax(i * 16 + fq * 4 + r);
+    int8_t* dst = &sQ[(i * 16 + fq * 4 + qk) * kQPitch + cb1 * 16 + (fr & 12)];
+#pragma unroll
+    for (int j = 0; j < kUpCB; j++) {
+      const uint32_t col4 = pack4(qround_bounded(__int_as_float(acc[i][j][0]) * inv_scale[0]),
+                                  qround_bounded(__int_as_float(acc[i][j][1]) * inv_scale[1]),
+                                  qround_bounded(__int_as_float(acc[i][j][2]) * inv_scale[2]),
+                                  qround_bounded(__int_as_float(acc[i][j][3]) * inv_scale[3]));
+      *reinterpret_cast<uint32_t*>(dst + j * 16) = quad_transpose_bytes(col4, qk);
+    }
+  }
+
+  // ---- FFN-down: acc2[i][j] = rows 16i.., columns (3w + j)*16.., K = 1536 ----
+  const int cb2 = wave * kDnCB;
+  const int8_t* w2 = p.w2 + (size_t)lane * 16;
+  auto load_b2 = [&](int kt, v4i* dst) {
+#pragma unroll
+    for (int j = 0; j < kDnCB; j++)
+      dst[j] = *reinterpret_cast<const v4i*>(w2 + ((size_t)kt * (kH / 16) + cb2 + j) * 1024);
+  };
+  v4i ring[kRing][kDnCB];
+#pragma unroll
+  for (int s = 0; s < kRing; s++) load_b2(s, ring[s]);
+  // the epilogue's residual float4s, loaded now so that HBM latency hides behind FFN-down
+  constexpr int kF4 = kDnCB * 4;              // float4 columns of one wave row (12)
+  constexpr int kEpiIt = kRows * kF4 / 64;    // float4s per lane (6)
+  float4 res4[kEpiIt];
+#pragma unroll
+  for (int k = 0; k < kEpiIt; k++) {
+    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx - rr * kF4;
+    const v4i r = __builtin_nontemporal_load(
+        reinterpret_cast<const v4i*>(p.res + (size_t)min(m0 + rr, p.M - 1) * kH + cb2 * 16 + c4 * 4));
+    res4[k] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z), __int_as_float(r.w));
+  }
+  __syncthreads();  // sQ complete
+  v4i acc2[2][kDnCB];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < kDnCB; j++) acc2[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int kt = 0; kt < kDnSteps; kt++) {  // fully unrolled ring of kRing steps
+    v4i af[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&sQ[(i * 16 + fr) * kQPitch + kt * 64 + fq * 16]);
+#pragma unroll
+    for (int j = 0; j < kDnCB; j++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        acc2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], ring[kt % kRing][j], acc2[i][j], 0, 0, 0);
+    if (kt + kRing < kDnSteps) load_b2(kt + kRing, ring[kt % kRing]);
+  }
+
+  // ---- epilogue of FFN-down through this wave's LDS tile, whole float4s per lane ----
+  int* E = sE[wave];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < kDnCB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) E[(i * 16 + fq * 4 + r) * kEPitch + j * 16 + fr] = acc2[i][j][r];
+  wave_lds_sync();
+#pragma unroll
+  for (int k = 0; k < kEpiIt; k++) {
+    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx - rr * kF4;
+    const int row = m0 + rr;
+    const bool ok = row < p.M;
+    const int col = cb2 * 16 + c4 * 4;
+    const float s = row_absmax(rr) / 127.0f;  // scale = max_abs / 127.0
+    const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
+    const float4 ws4 = *reinterpret_cast<const float4*>(p.w2_scale + col);
+    float4 b4 = *reinterpret_cast<const float4*>(p.b2 + col);
+    const float4 r4 = res4[k];
+    b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+    float4 v;
+    v.x = fmaf((float)a4.x, s * ws4.x, b4.x);
+    v.y = fmaf((float)a4.y, s * ws4.y, b4.y);
+    v.z = fmaf((float)a4.z, s * ws4.z, b4.z);
+    v.w = fmaf((float)a4.w, s * ws4.w, b4.w);
+    if (ok)
+      __builtin_nontemporal_store(v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)},
+                                  reinterpret_cast<v4i*>(p.out + (size_t)row * kH + col));
+  }
+}
+
+void launch_ffn(const FfnArgs& p, hipStream_t st) {
+  if (p.M <= 0) return;
+  hipLaunchKernelGGL(ffn_fused_kernel, dim3((p.M + kRows - 1) / kRows), dim3(512), 0, st, p);
+}
+
+}  // namespace aek

@@ -38,6 +38,25 @@ void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
 // host: [N,K] row-major int8 -> the GEMM's fragment order [K/64][N/16][64][16] (out has N*K bytes)
 void swizzle_weights(int n, int k, const int8_t* w, int8_t* out);
 
+// The FFN block of one layer in one kernel (hidden 384, intermediate 1536):
+// out = FFN-down(quant(GELU(FFN-up(A)) * g_smooth)) + b2 + res, with the
+// arithmetic of launch_gemm's kAI8/kEpiGelu and kAF32Q/kEpiF32 variants.
+struct FfnArgs {
+  int M;
+  const int8_t* A;         // [M,384]
+  const float* a_scale;    // [M]
+  const int8_t* w1;        // FFN-up, swizzled [1536,384]
+  const float* w1_scale;   // [1536]
+  const float* b1;         // [1536]
+  const float* g_smooth;   // FFN-down inv_smooth [1536]
+  const int8_t* w2;        // FFN-down, swizzled [384,1536]
+  const float* w2_scale;   // [384]
+  const float* b2;         // [384]
+  const float* res;        // [M,384] (may equal out)
+  float* out;              // [M,384]
+};
+void launch_ffn(const FfnArgs& p, hipStream_t st);
+
 constexpr int kLnSrcF32 = 0;
 constexpr int kLnSrcEmb = 1;
 struct LnArgs {

@@ -119,6 +119,31 @@ def test_gemm_gelu_epilogue_bit_exact(torch_gpu, m):
     assert np.array_equal(rowmax / f32(127), sc)
 
 
+@pytest.mark.parametrize("m,in_place", [(1, False), (31, False), (33, True), (100, False), (4133, True)])
+def test_ffn_fused_bit_exact(torch_gpu, m, in_place):
+    """The one-kernel FFN block (FFN-up + GELU * inv_smooth + row absmax int8
+    quantization + FFN-down + bias + residual) against the oracle's three steps
+    (src/model.rs:725-755): bit-exact, including partial last workgroups and
+    out == res."""
+    torch = torch_gpu
+    w1, ws1, b1, s1 = linear_inputs(1536, 384, 7)
+    w2, ws2, b2, s2 = linear_inputs(384, 1536, 8)
+    rng = np.random.default_rng(m + 11)
+    a = rng.integers(-127, 128, (m, 384), dtype=np.int8)
+    a[0, :] = 0  # a row whose GELU outputs are GELU(bias) only
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    res = rng.normal(0, 1, (m, 384)).astype(f32)
+    up, down = ae.Linear(w1, ws1, b1, s1), ae.Linear(w2, ws2, b2, s2)
+    a_d, sa_d, res_d = dev(torch, a), dev(torch, sa), dev(torch, res)
+    out_d = res_d if in_place else torch.full((m, 384), float("nan"), dtype=torch.float32, device="cuda")
+    up.ffn(down, m, a_d.data_ptr(), sa_d.data_ptr(), res_d.data_ptr(), out_d.data_ptr())
+    torch.cuda.synchronize()
+    pre = orc.gemm(a, sa, w1, ws1, b1)
+    _, q, sc = orc.gelu_quant_rows(pre, s2)  # src/simd_math.rs:1295-1312
+    ref = orc.gemm(q, sc, w2, ws2, b2, res)
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
+
+
 @pytest.mark.parametrize("m", [1, 31, 33, 100])
 def test_layernorm_quant_bit_exact(torch_gpu, m):
     torch = torch_gpu
