@@ -248,7 +248,7 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
     v.y = fmaf((float)a4.y, s * ws4.y, b4.y);
     v.z = fmaf((float)a4.z, s * ws4.z, b4.z);
     v.w = fmaf((float)a4.w, s * ws4.w, b4.w);
-    if (ok)
+    if (ok)  // streaming store: keeps the weights resident in L2
       __builtin_nontemporal_store(v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)},
                                   reinterpret_cast<v4i*>(p.out + (size_t)row * kH + col));
   }

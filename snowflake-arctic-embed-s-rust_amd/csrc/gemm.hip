@@ -213,7 +213,8 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
       const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
       float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
       if (p.res) {
-        const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)rrow * p.N + col);
+        const v4i r4i = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.res + (size_t)rrow * p.N + col));
+        const float4 r4 = make_float4(__int_as_float(r4i.x), __int_as_float(r4i.y), __int_as_float(r4i.z), __int_as_float(r4i.w));
         b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
       }
       float4 v;
