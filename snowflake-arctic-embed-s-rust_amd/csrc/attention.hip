@@ -71,6 +71,17 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
 // blk*16 + n; result r holds block r/4, row m = 4*(l/16) + r%4, column n = l%16.
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+// Element loads from this workgroup's rows of the packed qkv buffer through a
+// buffer resource: the row offset (wave-uniform) is a scalar and the lane's
+// column offset one VGPR shared by every load, so a load costs no vector
+// address arithmetic.  Raw buffer, gfx9 descriptor word 3 (32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float* base, int rows) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, rows * HQKV * 4, 0x00020000);
+}
+__device__ __forceinline__ float row_load(__amdgpu_buffer_rsrc_t r, uint32_t lane_bytes, uint32_t row) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, row * (uint32_t)(HQKV * 4), 0));
+}
+
 __device__ __forceinline__ v16f mfma_products(float a, float b) {
   const v16f zero = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, zero, 0, 0, 0);
@@ -175,8 +186,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     sc.z = acc[2] * kInvSqrtD;
     sc.w = acc[3] * kInvSqrtD;
     *reinterpret_cast<float4*>(srow + t) = sc;  // t + 3 < round16(L) <= pitch - 4
-    if (t + 3 < L) {
-      m = fmaxf(fmaxf(m, sc.x), fmaxf(sc.y, fmaxf(sc.z, sc.w)));
+    // a key t >= L was computed from K row L - 1 (clamped), so its score repeats
+    // key L - 1's bit for bit and cannot change the max: no mask needed.  (The
+    // narrow layout keeps the masked form: without it the compiler schedules its
+    // loop into 145 VGPRs instead of 90.)
+    if (kWide || t + 3 < L) {
+      m = fmaxf(fmaxf(m, fmaxf(sc.x, sc.y)), fmaxf(sc.z, sc.w));
     } else {
       if (t < L) m = fmaxf(m, sc.x);
       if (t + 1 < L) m = fmaxf(m, sc.y);
@@ -316,10 +331,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     // group are clamped to it (wave-uniform), so every load is unconditional and
     // the main loop has no early exit.
     const int Lf = L & ~15, ng = Lf >> 4;
+    const __amdgpu_buffer_rsrc_t vbuf = rows_rsrc(qkv, L);
     auto load_v = [&](int g, float (&v)[4]) {
       const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
 #pragma unroll
-      for (int u = 0; u < 4; u++) v[u] = qkv[(t0 + (kWide ? u : 4 * u)) * (uint32_t)HQKV + voff];
+      for (int u = 0; u < 4; u++) v[u] = row_load(vbuf, 4 * voff, t0 + (kWide ? u : 4 * u));
     };
     auto load_p = [&](int g) {
       const float* e = prow + 16 * min(g, ng - 1);
@@ -352,9 +368,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     if (!kWide) {
       // one group per step through the ring (fewer registers, for short rows)
       auto load_vn = [&](int g, float (&v)[4]) {
-        const float* src = qkv + (size_t)(16 * min(g, ng - 1)) * HQKV + voff;
+        const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
 #pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = src[(size_t)(4 * u) * HQKV];
+        for (int u = 0; u < 4; u++) v[u] = row_load(vbuf, 4 * voff, t0 + 4 * u);
       };
       auto pv_narrow = [&](int g, const float (&v)[4]) {  // P read as the MFMAs go
 #pragma unroll
