@@ -53,6 +53,7 @@ typedef struct ae_engine ae_engine;       /* ArcticEmbedS, src/lib.rs:34-38 */
 typedef struct ae_workspace ae_workspace; /* Workspace, src/model.rs:123-173 */
 typedef struct ae_linear ae_linear;       /* PackedLinearInt8, src/gemm.rs:165-181 */
 typedef struct ae_tokenizer ae_tokenizer; /* BertTokenizer, src/tokenizer.rs:26-31 */
+typedef struct ae_parallel_context ae_parallel_context; /* ParallelContext, src/parallel.rs:137-142 */
 
 /* Human-readable text of the last error raised on the calling thread. */
 const char* ae_last_error(void);
@@ -111,6 +112,23 @@ int ae_embed_batch_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* 
 int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev,
                              const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
                              int max_seq_len, float* out_dev, void* stream);
+
+/* ---- latency mode: one sequence at a time ------------------------------- */
+/* ParallelContext::new(n_threads) (src/parallel.rs:144-160): n_threads is clamped
+ * to 1..8 as there and only recorded; the device parallelizes the sequence.  The
+ * context holds a single-sequence workspace for `e` (512 tokens, own stream,
+ * graph replay per length); use it from one thread at a time. */
+int ae_parallel_context_create(const ae_engine* e, int n_threads, ae_parallel_context** out);
+void ae_parallel_context_destroy(ae_parallel_context* c);
+/* the clamped thread count */
+int ae_parallel_context_threads(const ae_parallel_context* c);
+/* ArcticEmbedS::embed_tokens_parallel / embed_query_parallel /
+ * embed_document_parallel (src/lib.rs:104-133): same results as ae_embed_tokens /
+ * ae_embed_query / ae_embed_document, bit for bit. */
+int ae_embed_tokens_parallel(const ae_engine* e, ae_parallel_context* c, const uint16_t* ids, size_t n,
+                             float* out384);
+int ae_embed_query_parallel(const ae_engine* e, ae_parallel_context* c, const char* utf8, float* out384);
+int ae_embed_document_parallel(const ae_engine* e, ae_parallel_context* c, const char* utf8, float* out384);
 
 /* ---- tokenizer (host only) ---------------------------------------------- */
 /* BertTokenizer::from_vocab_file (src/tokenizer.rs:34-37). */

@@ -79,6 +79,12 @@ _SIGS = {
     "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_gemm_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_ffn": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "ae_parallel_context_create": (_i32, [_vp, _i32, _c.POINTER(_vp)]),
+    "ae_parallel_context_destroy": (None, [_vp]),
+    "ae_parallel_context_threads": (_i32, [_vp]),
+    "ae_embed_tokens_parallel": (_i32, [_vp, _vp, _vp, _sz, _vp]),
+    "ae_embed_query_parallel": (_i32, [_vp, _vp, _c.c_char_p, _vp]),
+    "ae_embed_document_parallel": (_i32, [_vp, _vp, _c.c_char_p, _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -251,6 +257,26 @@ class Engine:
                                    out.ctypes.data))
         return out
 
+    # --- latency mode (src/lib.rs:104-133) ---
+    def parallel_context(self, n_threads):
+        return ParallelContext(self, n_threads)
+
+    def embed_tokens_parallel(self, ids, par):
+        ids = np.ascontiguousarray(ids, dtype=np.uint16)
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_tokens_parallel(self._h, par.handle, ids.ctypes.data, ids.size, out.ctypes.data))
+        return out
+
+    def embed_query_parallel(self, text, par):
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_query_parallel(self._h, par.handle, text.encode("utf-8"), out.ctypes.data))
+        return out
+
+    def embed_document_parallel(self, text, par):
+        out = np.zeros(HIDDEN, dtype=np.float32)
+        _check(_lib.ae_embed_document_parallel(self._h, par.handle, text.encode("utf-8"), out.ctypes.data))
+        return out
+
     def forward_prefix(self, ws, seqs, layers):
         """Embedding + `layers` encoder layers; returns (hidden, act_q, act_scale) over packed rows."""
         ids, offsets = _pack_ids(list(seqs))
@@ -303,6 +329,34 @@ class Workspace:
     def close(self):
         if self._h:
             _lib.ae_workspace_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ParallelContext:
+    """ParallelContext (src/parallel.rs:137-253): latency mode for one sequence at a time."""
+
+    def __init__(self, engine, n_threads):
+        h = ctypes.c_void_p()
+        _check(_lib.ae_parallel_context_create(engine.handle, int(n_threads), ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def threads(self):
+        return int(_lib.ae_parallel_context_threads(self._h))
+
+    def close(self):
+        if self._h:
+            _lib.ae_parallel_context_destroy(self._h)
             self._h = None
 
     def __del__(self):

@@ -709,6 +709,47 @@ int ae_embed_batch(const ae_engine* e, ae_workspace* ws, const char* const* text
   return embed_texts(e, ws, texts, n, is_query != 0, num_threads, out);
 }
 
+// ParallelContext (src/parallel.rs:137-253): the reference's latency mode, which
+// spreads the forward pass of one sequence over 1..8 host threads.  On the
+// device the parallelism comes from the kernels themselves, so the context is a
+// single-sequence workspace (512 tokens, its own stream, one captured hipGraph
+// per sequence length) and the thread count is recorded only.  Results equal the
+// workspace path bit for bit (the same kernels on the same batch of one).
+struct ae_parallel_context {
+  int n_threads = 1;
+  ae_workspace* ws = nullptr;
+  ~ae_parallel_context() { ae_workspace_destroy(ws); }
+};
+
+int ae_parallel_context_create(const ae_engine* e, int n_threads, ae_parallel_context** out) {
+  if (!e || !out) return fail(AE_ERR_INVALID_ARG, "null argument");
+  *out = nullptr;
+  std::unique_ptr<ae_parallel_context> c(new ae_parallel_context());
+  c->n_threads = std::min(std::max(n_threads, 1), 8);  // ParallelContext::new clamps to 1..8 (src/parallel.rs:146)
+  if (int rc = ae_workspace_create(e, ae::kMaxPos, 1, &c->ws)) return rc;
+  *out = c.release();
+  return AE_OK;
+}
+
+void ae_parallel_context_destroy(ae_parallel_context* c) { delete c; }
+
+int ae_parallel_context_threads(const ae_parallel_context* c) { return c ? c->n_threads : 0; }
+
+int ae_embed_tokens_parallel(const ae_engine* e, ae_parallel_context* c, const uint16_t* ids, size_t n, float* out384) {
+  if (!c) return fail(AE_ERR_INVALID_ARG, "null parallel context");
+  return ae_embed_tokens(e, c->ws, ids, n, out384);
+}
+
+int ae_embed_query_parallel(const ae_engine* e, ae_parallel_context* c, const char* utf8, float* out384) {
+  if (!c) return fail(AE_ERR_INVALID_ARG, "null parallel context");
+  return ae_embed_query(e, c->ws, utf8, out384);
+}
+
+int ae_embed_document_parallel(const ae_engine* e, ae_parallel_context* c, const char* utf8, float* out384) {
+  if (!c) return fail(AE_ERR_INVALID_ARG, "null parallel context");
+  return ae_embed_document(e, c->ws, utf8, out384);
+}
+
 int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev, const int32_t* cu_seqlens_dev,
                              int n_seqs, int total_tokens, int max_seq_len, float* out_dev, void* stream) {
   if (!e || !ws || ws->e != e) return fail(AE_ERR_INVALID_ARG, "engine/workspace mismatch");

@@ -114,6 +114,48 @@ def test_text_api(engine, ws):
     assert engine.embed_batch(ws, []).shape == (0, 384)
 
 
+def test_parallel_context_matches_workspace(engine, ws):
+    """Latency mode (src/lib.rs:104-133) at the lengths and thread counts of the
+    reference's tests/parallel_test.rs: embed_tokens_parallel equals embed_tokens bit
+    for bit, on every call (eager, then graph capture, then replay)."""
+    lengths = [1, 2, 5, 8, 15, 16, 17, 31, 33, 64, 100, 128, 257, 512]
+    for threads in (2, 3, 4):
+        par = engine.parallel_context(threads)
+        assert par.threads == threads
+        for n in lengths:
+            ids = np.array([101] + [1996 + (i * 37) % 5000 for i in range(max(0, n - 2))] + ([102] if n >= 2 else []),
+                           np.uint16)
+            single = engine.embed_tokens(ws, ids)
+            for call in range(3):
+                multi = engine.embed_tokens_parallel(ids, par)
+                assert np.array_equal(single.view(np.uint32), multi.view(np.uint32)), (threads, n, call)
+        par.close()
+
+
+def test_parallel_context_fresh_and_text(engine, ws):
+    """Fresh contexts give the workspace result on their first call (the reference's
+    test_fresh_contexts_first_call_completes); thread counts clamp to 1..8; the text
+    entry points match embed_query / embed_document."""
+    ids = np.array([101, 2023, 2003, 1037, 3231, 102], np.uint16)
+    single = engine.embed_tokens(ws, ids)
+    for i in range(20):
+        par = engine.parallel_context(2 + i % 3)
+        assert np.array_equal(engine.embed_tokens_parallel(ids, par), single), i
+        par.close()
+    for n, want in ((0, 1), (-3, 1), (8, 8), (99, 8)):
+        par = engine.parallel_context(n)
+        assert par.threads == want
+        par.close()
+    par = engine.parallel_context(4)
+    q = "what is snowflake?"
+    d = "Snowflake's Data Cloud"
+    assert np.array_equal(engine.embed_query_parallel(q, par), engine.embed_query(ws, q))
+    assert np.array_equal(engine.embed_document_parallel(d, par), engine.embed_document(ws, d))
+    with pytest.raises(ae.AeError):
+        engine.embed_tokens_parallel(np.zeros(0, np.uint16), par)
+    par.close()
+
+
 def test_errors(engine, ws):
     with pytest.raises(ae.AeError) as e:
         engine.embed_tokens(ws, np.zeros(0, np.uint16))
