@@ -149,6 +149,33 @@ __device__ __forceinline__ float gelu_exact(float x, const ExpTab& tb) {
   return 0.5f * x * (1.0f + erf_val);
 }
 
+// Sequential sum of f(row[j]) over one 384-float LDS row (float4-aligned), in
+// index order: 12 batches of 8 float4, each read while the previous one is added.
+template <typename F>
+__device__ __forceinline__ float lds_row_sum(const float* row, F f) {
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+  float4 va[8], vb[8];
+  auto ld = [&](int bi, float4 (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = r4[8 * min(bi, 11) + i];
+  };
+  float acc = 0.0f;
+  auto add = [&](const float4 (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      acc += f(v[i].x); acc += f(v[i].y); acc += f(v[i].z); acc += f(v[i].w);
+    }
+  };
+  ld(0, va);
+  for (int bi = 0; bi < 12; bi += 2) {
+    ld(bi + 1, vb);
+    add(va);
+    ld(bi + 2, va);
+    add(vb);
+  }
+  return acc;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (WG p -> XCD p % 8),
 // each with its own L2.  xcd_contiguous(p, n) renumbers the n workgroups of a
 // launch so that XCD x runs one contiguous range of logical items: neighbouring

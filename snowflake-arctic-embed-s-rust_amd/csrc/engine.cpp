@@ -313,9 +313,8 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     (void)hipStreamSynchronize(st);
     drain_timing(ws);
   }
-  auto gemm = [&](const ae_linear& L, int M, const void* A, int amode, const float* a_scale, const uint32_t* a_rowmax,
-                  const float* a_smooth, const float* res, float* o, int emode, const float* g_smooth,
-                  uint32_t* g_rowmax) {
+  auto gemm_args = [&](const ae_linear& L, int M, const void* A, const float* a_scale, const uint32_t* a_rowmax,
+                       const float* a_smooth, const float* res, float* o, const float* g_smooth, uint32_t* g_rowmax) {
     GemmArgs p{};
     p.M = M;
     p.N = L.n;
@@ -333,10 +332,15 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.g_rowmax = g_rowmax;
     p.partial = ws->splitk;
     p.partial_ints = ws->splitk_ints;
-    launch_gemm(p, amode, emode, st);
+    return p;
   };
-  auto ln = [&](const float* src, float* dst, const float* gw, const float* gb, const float* smooth, int8_t* q,
-                float* scale, uint32_t* rowmax_init, int rows) {
+  auto gemm = [&](const ae_linear& L, int M, const void* A, int amode, const float* a_scale, const uint32_t* a_rowmax,
+                  const float* a_smooth, const float* res, float* o, int emode, const float* g_smooth,
+                  uint32_t* g_rowmax) {
+    launch_gemm(gemm_args(L, M, A, a_scale, a_rowmax, a_smooth, res, o, g_smooth, g_rowmax), amode, emode, st);
+  };
+  auto ln_args = [&](const float* src, float* dst, const float* gw, const float* gb, const float* smooth, int8_t* q,
+                     float* scale, uint32_t* rowmax_init, int rows) {
     LnArgs p{};
     p.T = rows;
     p.src = src;
@@ -347,7 +351,22 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.q = q;
     p.scale = scale;
     p.rowmax_init = rowmax_init;
-    launch_ln_quant(p, kLnSrcF32, st);
+    return p;
+  };
+  // an N = 384 GEMM and the LayerNorm of its output: one fused split-K epilogue
+  // when the GEMM splits K (few rows, latency-bound), else the two kernels
+  auto gemm_then_ln = [&](int gemm_kind, int ln_kind, const GemmArgs& g, int amode, const LnArgs& l) {
+    if (gemm_splits_k(g)) {
+      KernelTimer kt(ws, st, gemm_kind);
+      launch_gemm_ln(g, amode, l, st);
+      return;
+    }
+    {
+      KernelTimer kt(ws, st, gemm_kind);
+      launch_gemm(g, amode, kEpiF32, st);
+    }
+    KernelTimer kt(ws, st, ln_kind);
+    launch_ln_quant(l, kLnSrcF32, st);
   };
   {  // embeddings + LayerNorm + SmoothQuant (src/model.rs:549-586)
     KernelTimer kt(ws, st, AE_KERNEL_EMBED_LN);
@@ -383,34 +402,31 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
       launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
     }
-    {
-      KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
-      gemm(D.attn_out, T, ws->ctx, kAF32QSmooth, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
-           kEpiF32, nullptr, nullptr);
-    }
-    {
-      KernelTimer kt(ws, st, AE_KERNEL_LN1);
-      ln(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale, ws->rowmax_g, T);
-    }
+    gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1,
+                 gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
+                           nullptr, nullptr),
+                 kAF32QSmooth,
+                 ln_args(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale,
+                         ws->rowmax_g, T));
+    const LnArgs ln2 = ln_args(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q,
+                               ws->act_scale, ws->rowmax_ctx, T);
     if (T >= kFfnFusedMinRows) {  // FFN-up, GELU, quantize and FFN-down in one kernel
-      KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
-      launch_ffn(ffn_args(D.ffn_inter, D.ffn_out, T, ws->act_q, ws->act_scale, ws->hidden, ws->tmp), st);
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
+        launch_ffn(ffn_args(D.ffn_inter, D.ffn_out, T, ws->act_q, ws->act_scale, ws->hidden, ws->tmp), st);
+      }
+      KernelTimer kt(ws, st, AE_KERNEL_LN2);
+      launch_ln_quant(ln2, kLnSrcF32, st);
     } else {
       {
         KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
         gemm(D.ffn_inter, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->g, kEpiGelu,
              D.ffn_out.inv_smooth, ws->rowmax_g);
       }
-      {
-        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
-        gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
-             nullptr);
-      }
-    }
-    {
-      KernelTimer kt(ws, st, AE_KERNEL_LN2);
-      ln(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q, ws->act_scale,
-         ws->rowmax_ctx, T);
+      gemm_then_ln(AE_KERNEL_GEMM_FFN_DOWN, AE_KERNEL_LN2,
+                   gemm_args(D.ffn_out, T, ws->g, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, nullptr,
+                             nullptr),
+                   kAF32Q, ln2);
     }
   }
   if (stop_layers >= 0) {
@@ -440,9 +456,18 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   launch_cls(c, 0, st);
   gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
   launch_cls(c, 1, st);
-  gemm(D.attn_out, B, ws->ctx_c, kAF32QSmooth, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth, ws->hidden_c,
-       ws->tmp_c, kEpiF32, nullptr, nullptr);
-  ln(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c, ws->act_scale_c, ws->rowmax_g_c, B);
+  {
+    const GemmArgs g = gemm_args(D.attn_out, B, ws->ctx_c, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth,
+                                 ws->hidden_c, ws->tmp_c, nullptr, nullptr);
+    const LnArgs l = ln_args(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c,
+                             ws->act_scale_c, ws->rowmax_g_c, B);
+    if (gemm_splits_k(g)) {
+      launch_gemm_ln(g, kAF32QSmooth, l, st);
+    } else {
+      launch_gemm(g, kAF32QSmooth, kEpiF32, st);
+      launch_ln_quant(l, kLnSrcF32, st);
+    }
+  }
   gemm(D.ffn_inter, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->g_c, kEpiGelu,
        D.ffn_out.inv_smooth, ws->rowmax_g_c);
   gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->tmp_c, ws->hidden_c, kEpiF32, nullptr,

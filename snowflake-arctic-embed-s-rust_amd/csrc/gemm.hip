@@ -288,6 +288,88 @@ __global__ __launch_bounds__(256) void gemm_splitk_epilogue_kernel(GemmArgs p) {
   if (in) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
 }
 
+// Split-K epilogue of an N = 384 GEMM (kEpiF32) with the LayerNorm +
+// SmoothQuant of each output row fused: ln_quant_kernel's arithmetic in the
+// same order (layernorm_smooth_quantize_row_scalar, reference
+// src/simd_math.rs:208-247), one 128-thread block per row.  The GEMM output row
+// stays in LDS; only the LayerNorm results (ln.dst, ln.q, ln.scale) are stored.
+// ln.dst may equal p.res: each block reads its residual row before the barrier
+// that precedes its stores.
+template <int AM>
+__global__ __launch_bounds__(128) void gemm_splitk_epilogue_ln_kernel(GemmArgs p, LnArgs ln) {
+  __shared__ __attribute__((aligned(16))) float xrow[384];
+  __shared__ float s_stat[2], s_amax[2];
+  const int row = blockIdx.x, t = threadIdx.x;
+  const bool own = t < 96;  // float4 column 4t of the row
+  const int col = 4 * min(t, 95);
+  if (own) {
+    int4 a4 = make_int4(0, 0, 0, 0);
+    for (int sp = 0; sp < p.ksplit; sp++) {
+      const int4 v = *reinterpret_cast<const int4*>(p.partial + ((size_t)sp * p.M + row) * 384 + col);
+      a4.x += v.x; a4.y += v.y; a4.z += v.z; a4.w += v.w;
+    }
+    float sa;
+    if (AM == kAI8) sa = p.a_scale[row];
+    else sa = __uint_as_float(p.a_rowmax[row]) / 127.0f;  // scale = max_abs / 127.0
+    const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
+    float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
+    if (p.res) {
+      const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)row * 384 + col);
+      b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+    }
+    float4 v;
+    v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
+    v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
+    v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
+    v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
+    *reinterpret_cast<float4*>(&xrow[col]) = v;
+  }
+  __syncthreads();
+  if (t == 0) {  // sequential sums over the row, in index order
+    const float mean = lds_row_sum(xrow, [](float x) { return x; }) / 384.0f;
+    const float var_sum = lds_row_sum(xrow, [mean](float x) {
+      const float d = x - mean;
+      return d * d;
+    });
+    s_stat[0] = mean;
+    s_stat[1] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
+  }
+  __syncthreads();
+  const float mean = s_stat[0], rstd = s_stat[1];
+  const float4 x = *reinterpret_cast<const float4*>(&xrow[col]);
+  const float4 g = *reinterpret_cast<const float4*>(ln.gamma + col);
+  const float4 b = *reinterpret_cast<const float4*>(ln.beta + col);
+  const float4 sm = *reinterpret_cast<const float4*>(ln.smooth + col);
+  float4 y;
+  y.x = (x.x - mean) * rstd * g.x + b.x;
+  y.y = (x.y - mean) * rstd * g.y + b.y;
+  y.z = (x.z - mean) * rstd * g.z + b.z;
+  y.w = (x.w - mean) * rstd * g.w + b.w;
+  if (own) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + col) = y;
+  const float4 ys = make_float4(y.x * sm.x, y.y * sm.y, y.z * sm.z, y.w * sm.w);
+  float amax = 0.0f;
+  if (own) {
+    amax = nanless_max(amax, fabsf(ys.x));
+    amax = nanless_max(amax, fabsf(ys.y));
+    amax = nanless_max(amax, fabsf(ys.z));
+    amax = nanless_max(amax, fabsf(ys.w));
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+  if ((t & 63) == 0) s_amax[t >> 6] = amax;
+  __syncthreads();
+  const float max_abs = nanless_max(1e-8f, nanless_max(s_amax[0], s_amax[1]));
+  const float inv_scale = 127.0f / max_abs;
+  if (own)
+    *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + col) =
+        pack4(qround(ys.x * inv_scale), qround(ys.y * inv_scale), qround(ys.z * inv_scale), qround(ys.w * inv_scale));
+  if (t == 0) {
+    ln.scale[row] = max_abs / 127.0f;
+    if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
+    if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
+  }
+}
+
 // Workgroups of 64 rows x 192 columns.  Small M (fewer than kSplitGrid
 // workgroups) splits K into ranges of at least two steps when the caller
 // provides int32 scratch (GemmArgs::partial) for the partial sums.
@@ -297,8 +379,7 @@ constexpr int kSplitGrid = 192;
 // tile fastest, 25 MB at M = 65,536 up to 13 % slower)
 constexpr size_t kColFastABytes = size_t(96) << 20;
 
-template <int AM, int EM>
-static void launch_variant(GemmArgs p, hipStream_t st) {
+static int split_k(const GemmArgs& p) {
   const int mt = (p.M + kBM - 1) / kBM, nbase = mt * (p.N / 192), kt = p.K / 64;
   int ks = 1;
   if (p.partial && nbase < kSplitGrid) {
@@ -306,12 +387,38 @@ static void launch_variant(GemmArgs p, hipStream_t st) {
     ks = (int)std::min<size_t>((size_t)ks, p.partial_ints / ((size_t)p.M * p.N));
     if (ks < 2) ks = 1;
   }
-  p.ksplit = ks;
+  return ks;
+}
+
+// ln != null (N = 384, kEpiF32, split K): the epilogue also applies *ln to each
+// output row and p.out is not written
+template <int AM, int EM>
+static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullptr) {
+  const int nbase = ((p.M + kBM - 1) / kBM) * (p.N / 192);
+  p.ksplit = split_k(p);
   p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;
-  hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase * ks), dim3(256), 0, st, p);
-  if (ks > 1)
-    hipLaunchKernelGGL((gemm_splitk_epilogue_kernel<AM, EM>), dim3((p.N / 4 + 255) / 256, p.M), dim3(256), 0, st,
-                       p);
+  hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase * p.ksplit), dim3(256), 0, st, p);
+  if (p.ksplit > 1) {
+    if (ln) hipLaunchKernelGGL((gemm_splitk_epilogue_ln_kernel<AM>), dim3(p.M), dim3(128), 0, st, p, *ln);
+    else hipLaunchKernelGGL((gemm_splitk_epilogue_kernel<AM, EM>), dim3((p.N / 4 + 255) / 256, p.M), dim3(256), 0,
+                            st, p);
+  }
+}
+
+bool gemm_splits_k(const GemmArgs& p) { return p.M > 0 && split_k(p) > 1; }
+
+void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {
+  if (p.M <= 0) return;
+  if (p.N != 384 || split_k(p) < 2) {  // no split: the GEMM, then the LayerNorm kernel over its output
+    launch_gemm(p, amode, kEpiF32, st);
+    LnArgs l = ln;
+    l.src = p.out;
+    launch_ln_quant(l, kLnSrcF32, st);
+    return;
+  }
+  if (amode == kAI8) launch_variant<kAI8, kEpiF32>(p, st, &ln);
+  else if (amode == kAF32Q) launch_variant<kAF32Q, kEpiF32>(p, st, &ln);
+  else if (amode == kAF32QSmooth) launch_variant<kAF32QSmooth, kEpiF32>(p, st, &ln);
 }
 
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st) {

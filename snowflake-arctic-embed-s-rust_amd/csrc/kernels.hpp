@@ -82,6 +82,13 @@ struct LnArgs {
   uint32_t* rowmax_init2;  // optional second buffer
 };
 void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st);
+// An N = 384 GEMM (kEpiF32) followed by the LayerNorm + SmoothQuant of its
+// output rows (ln.src is ignored: the GEMM output).  With split K the LayerNorm
+// runs in the split-K epilogue and p.out is not written; otherwise the GEMM
+// writes p.out and launch_ln_quant reads it.
+void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st);
+// whether launch_gemm splits K for these arguments (few rows and split-K scratch given)
+bool gemm_splits_k(const GemmArgs& p);
 
 void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, float* scale, bool gelu,
                       hipStream_t st);
