@@ -123,7 +123,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   const int nq = min(kAttnQ, L - q0);
   const int nqh = (nq + 15) >> 4;  // query halves with at least one query
   float* S = smem;                 // [kAttnQ][pitch]
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: per-wave loop bounds stay scalar
   const int lr = lane & 15, lg = lane >> 4;  // fragment row / block of this lane
   const ExpTab tb = exp_tab_regs();
   const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;

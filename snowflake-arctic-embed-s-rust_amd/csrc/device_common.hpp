@@ -81,9 +81,11 @@ static __constant__ uint64_t kExp2Tab[32] = {
 // The table lives in registers across the wave: lane l keeps entry l % 32 as two
 // 32-bit halves, and a lookup is a pair of ds_bpermute (a crossbar read of
 // another lane's register: no LDS bank conflicts, unlike a data-dependent
-// ds_read of a shared table).  A lookup reads lanes 0..31, so EVERY lane of the
-// wave must be active at every expf_libm / gelu_exact call: call them only
-// from wave-uniform control flow.
+// ds_read of a shared table).  ds_bpermute picks lane (address / 4) mod 64
+// (checked on gfx950), and both halves of the wave hold the table, so the
+// lookup of index k reads lane k mod 64 without masking k to 5 bits.  A lookup
+// may read any lane, so EVERY lane of the wave must be active at every
+// expf_libm / gelu_exact call: call them only from wave-uniform control flow.
 struct ExpTab {
   uint32_t lo, hi;
 };
@@ -93,8 +95,9 @@ __device__ __forceinline__ ExpTab exp_tab_regs() {
   return ExpTab{(uint32_t)t, (uint32_t)(t >> 32)};
 }
 
-__device__ __forceinline__ uint64_t exp_tab_lookup(const ExpTab& tb, uint32_t i) {
-  const int addr = (int)(i << 2);  // byte address of lane i
+// entry k % 32 (k: any 32-bit value)
+__device__ __forceinline__ uint64_t exp_tab_lookup(const ExpTab& tb, uint32_t k) {
+  const int addr = (int)(k << 2);  // byte address of lane k mod 64, which holds entry k % 32
   const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)tb.lo);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)tb.hi);
   return ((uint64_t)hi << 32) | lo;
@@ -118,7 +121,7 @@ __device__ __forceinline__ float expf_libm(float x, const ExpTab& tb) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  const uint64_t t = exp_tab_lookup(tb, (uint32_t)ki & 31u) + (ki << 47);
+  const uint64_t t = exp_tab_lookup(tb, (uint32_t)ki) + (ki << 47);
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(c0, r, c1);
   const double r2 = r * r;
