@@ -144,6 +144,39 @@ def test_ffn_fused_bit_exact(torch_gpu, m, in_place):
     assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
 
 
+def test_ffn_fused_extreme_rows(torch_gpu):
+    """The fused FFN on rows that drive the GELU to its extremes: saturated int8
+    rows (|pre-activation| up to ~1e3, GELU -> 0 or x), tiny scales (GELU near
+    0, the 1e-8 absmax floor), a single nonzero column, and rows of equal values
+    (quantization ties)."""
+    torch = torch_gpu
+    w1, ws1, b1, s1 = linear_inputs(1536, 384, 21)
+    w2, ws2, b2, s2 = linear_inputs(384, 1536, 22)
+    m = 40
+    rng = np.random.default_rng(23)
+    a = rng.integers(-127, 128, (m, 384), dtype=np.int8)
+    a[1:5] = 127
+    a[5:9] = -127
+    a[9] = 0
+    a[10] = 0
+    a[10, 17] = 127
+    a[11:14] = 64
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    sa[1:3] = 40.0                      # huge pre-activations
+    sa[14:18] = np.float32(1e-30)       # GELU inputs ~ bias only
+    sa[18] = 0.0
+    res = rng.normal(0, 1, (m, 384)).astype(f32)
+    up, down = ae.Linear(w1, ws1, b1, s1), ae.Linear(w2, ws2, b2, s2)
+    a_d, sa_d, res_d = dev(torch, a), dev(torch, sa), dev(torch, res)
+    out_d = torch.full((m, 384), float("nan"), dtype=torch.float32, device="cuda")
+    up.ffn(down, m, a_d.data_ptr(), sa_d.data_ptr(), res_d.data_ptr(), out_d.data_ptr())
+    torch.cuda.synchronize()
+    pre = orc.gemm(a, sa, w1, ws1, b1)
+    _, q, sc = orc.gelu_quant_rows(pre, s2)
+    ref = orc.gemm(q, sc, w2, ws2, b2, res)
+    assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
+
+
 @pytest.mark.parametrize("m", [1, 31, 33, 100])
 def test_layernorm_quant_bit_exact(torch_gpu, m):
     torch = torch_gpu
