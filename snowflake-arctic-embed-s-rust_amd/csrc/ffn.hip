@@ -126,6 +126,10 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
   const ExpTab tb = exp_tab_regs();  // wave-uniform from here to the end of the loop
 #pragma unroll
   for (int j = 0; j < kUpCB; j++) {
+    // waves w and w + 4 share a SIMD; alternating their priority per column block
+    // keeps them level, so neither waits long at the barrier after the loop
+    if ((j ^ (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
     const int col = (cb1 + j) * 16 + fr;
     const float ws = p.w1_scale[col], bb = p.b1[col], gs = p.g_smooth[col];
 #pragma unroll
@@ -142,6 +146,7 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
         mx[i][r] = nanless_max(mx[i][r], fabsf(g));
       }
   }
+  __builtin_amdgcn_s_setprio(0);
   // row absmax: over the 16 lanes of this row quad (no NaN: nanless_max above),
   // then over the 8 waves via LDS
 #pragma unroll
