@@ -85,35 +85,40 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
         __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.A + (size_t)grow * kH + c16 * 16));
   }
 
-  // ---- FFN-up: acc[i][j] = rows 16i.., columns (12w + j)*16.. ----
+  // ---- FFN-up and its GELU epilogue, software-pipelined by column block ----
+  // acc[i][j] = rows 16i.., columns (cb1 + j)*16..  Column block j is finished
+  // (all six K steps) one iteration before its GELU, and its weight fragments
+  // are loaded two iterations before that, so the matrix cores and the weight
+  // stream of block j + 1 run while the VALU evaluates the GELUs of block j.
   const int cb1 = wave * kUpCB;
   const int8_t* w1 = p.w1 + (size_t)lane * 16;
-  auto load_b1 = [&](int kt, v4i* dst) {
+  auto load_col = [&](int j, v4i* dst) {  // the six K steps of column block j
 #pragma unroll
-    for (int j = 0; j < kUpCB; j++)
-      dst[j] = *reinterpret_cast<const v4i*>(w1 + ((size_t)kt * (kF / 16) + cb1 + j) * 1024);
+    for (int kt = 0; kt < kUpSteps; kt++)
+      dst[kt] = *reinterpret_cast<const v4i*>(w1 + ((size_t)kt * (kF / 16) + cb1 + j) * 1024);
   };
-  v4i b1[2][kUpCB];
-  load_b1(0, b1[0]);
-  __syncthreads();
   v4i acc[2][kUpCB];
+  auto mma_col = [&](int j, const v4i* bf) {
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 2; i++) acc[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < kUpCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int kt = 0; kt < kUpSteps; kt++) {
+      v4i af[2];
 #pragma unroll
-  for (int kt = 0; kt < kUpSteps; kt++) {  // fully unrolled: the two fragment buffers alternate without copies
-    if (kt + 1 < kUpSteps) load_b1(kt + 1, b1[(kt + 1) & 1]);
-    v4i af[2];
+      for (int i = 0; i < 2; i++)
+        af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAPitch + kt * 64 + fq * 16]);
 #pragma unroll
-    for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAPitch + kt * 64 + fq * 16]);
-#pragma unroll
-    for (int j = 0; j < kUpCB; j++)
-#pragma unroll
-      for (int i = 0; i < 2; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], b1[kt & 1][j], acc[i][j], 0, 0, 0);
-  }
+      for (int i = 0; i < 2; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt], acc[i][j], 0, 0, 0);
+    }
+  };
+  v4i bq[2][kUpSteps];  // fragments of column blocks j + 1 (then j + 3) and j + 2
+  load_col(0, bq[0]);
+  load_col(1, bq[1]);
+  __syncthreads();  // the input tile is in LDS
+  mma_col(0, bq[0]);
+  load_col(2, bq[0]);
 
-  // ---- epilogue of FFN-up: g = GELU(fma(f32(acc), sa*ws, b)) * inv_smooth, in place ----
+  // GELU epilogue: g = GELU(fma(f32(acc), sa*ws, b)) * inv_smooth, in place.
   // This lane holds rows 16i + 4fq + r (i < 2, r < 4) of column (cb1 + j)*16 + fr.
   float sa[2][4], mx[2][4];
 #pragma unroll
@@ -130,6 +135,10 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
     // keeps them level, so neither waits long at the barrier after the loop
     if ((j ^ (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
     else __builtin_amdgcn_s_setprio(0);
+    if (j + 1 < kUpCB) {
+      mma_col(j + 1, bq[(j + 1) & 1]);
+      if (j + 3 < kUpCB) load_col(j + 3, bq[(j + 1) & 1]);
+    }
     const int col = (cb1 + j) * 16 + fr;
     const float ws = p.w1_scale[col], bb = p.b1[col], gs = p.g_smooth[col];
 #pragma unroll
