@@ -322,6 +322,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   const bool has_item = qh < nqh;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (has_item) {
+    // the output's inv_smooth, loaded ahead of the PV loop
+    const float sm = p.rowmax ? p.smooth[h * 32 + 16 * dh + lr] : 0.0f;
     const float* prow = &S[(16 * qh + lr) * pitch];
     const float inv = s_inv[16 * qh + lr];
     const int vcol = 2 * H + 16 * dh + lr;
@@ -346,13 +348,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
         return float4{e[lg], e[4 + lg], e[8 + lg], e[12 + lg]};  // keys t0 + 4u + lg
       }
     };
-    auto pv_group = [&](const float4& e4, const float (&v)[4]) {
-      v16f pr[4];
+    // one group of 16 keys: p[u] and v[u] are the operands of MFMA u
+    auto pv_add = [&](const float (&pu)[4], const float (&v)[4]) {
       if constexpr (kWide) {
-        pr[0] = mfma_products(e4.x * inv, v[0]);
-        pr[1] = mfma_products(e4.y * inv, v[1]);
-        pr[2] = mfma_products(e4.z * inv, v[2]);
-        pr[3] = mfma_products(e4.w * inv, v[3]);
+        v16f pr[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) pr[u] = mfma_products(pu[u], v[u]);
 #pragma unroll
         for (int blk = 0; blk < 4; blk++)
 #pragma unroll
@@ -360,12 +361,28 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[i] = acc[i] + pr[u][4 * blk + i];
       } else {
-        add_blocks(acc, mfma_products(e4.x * inv, v[0]));
-        add_blocks(acc, mfma_products(e4.y * inv, v[1]));
-        add_blocks(acc, mfma_products(e4.z * inv, v[2]));
-        add_blocks(acc, mfma_products(e4.w * inv, v[3]));
+#pragma unroll
+        for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(pu[u], v[u]));
       }
     };
+    auto pv_group = [&](const float4& e4, const float (&v)[4]) {
+      const float pu[4] = {e4.x * inv, e4.y * inv, e4.z * inv, e4.w * inv};
+      pv_add(pu, v);
+    };
+    // The last L - Lf (< 16) keys form one more group, masked: keys past the
+    // segment get p = v = +0, whose +0 products leave the sum unchanged (it
+    // starts at +0, so it is never -0).  Its V is loaded here, before the main
+    // loop, with the rows clamped per lane; tail_key(u) is this lane's key of
+    // MFMA u.
+    const bool tail = L > Lf;  // wave-uniform
+    auto tail_key = [&](int u) { return Lf + (kWide ? 4 * lg + u : 4 * u + lg); };
+    float vt[4];
+    if (tail) {
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        vt[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            vbuf, (uint32_t)(min(tail_key(u), L - 1) * HQKV + vcol) * 4u, 0, 0));
+    }
     if (!kWide) {
       // one group per step through the ring (fewer registers, for short rows)
       auto load_vn = [&](int g, float (&v)[4]) {
@@ -429,27 +446,36 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
       }
       if (g + 2 < ng) pv_group(pa, v2);
     }
-    // last L - Lf (< 16) keys: keys past the segment contribute exact zeros
-    for (int t0 = Lf; t0 < L; t0 += 4) {
-      const int t = t0 + lg;
-      const bool in = t < L;
-      const float e = prow[min(t, L - 1)];
-      const float v = (qkv + (size_t)min(t, L - 1) * HQKV)[vcol];
-      add_blocks(acc, mfma_products(in ? e * inv : 0.0f, in ? v : 0.0f));
+    if (tail) {
+      // keys up to Lf + 15 < round16(L) <= pitch - 4 stay inside the score row
+      float pu[4], vu[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int t = tail_key(u);
+        pu[u] = t < L ? prow[t] * inv : 0.0f;
+        vu[u] = t < L ? vt[u] : 0.0f;
+      }
+      pv_add(pu, vu);
     }
-  }
-  if (has_item) {
-    const int d = 16 * dh + lr;
-    const float sm = p.rowmax ? p.smooth[h * 32 + d] : 0.0f;
+
+    // Lane l holds queries qb .. qb + 3 at dim d.  With `rowmax`, each query's
+    // max |ctx * inv_smooth| over this wave's 16 dims (one DPP row; every value
+    // is a non-NaN >= +0, where fmaxf is the reference's `if a > max` scan) goes
+    // to rowmax by atomicMax on its f32 bits.  All stores are issued last, with
+    // no wait between them.
+    const int qb = 16 * qh + 4 * lg, d = 16 * dh + lr;
+    float* out = p.ctx + (size_t)(s0 + q0 + qb) * H + h * 32 + d;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = 16 * qh + 4 * lg + i;
-      if (q < nq) p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = acc[i];
-      if (p.rowmax) {
-        float a = nanless_max(0.0f, fabsf(acc[i] * sm));
+    for (int i = 0; i < 4; i++)
+      if (qb + i < nq) out[(size_t)i * H] = acc[i];
+    if (p.rowmax) {
+      float a[4];
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
-        if (q < nq && lr == 0) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
+      for (int i = 0; i < 4; i++) a[i] = row16_max(nanless_max(0.0f, fabsf(acc[i] * sm)));
+      if (lr == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (qb + i < nq) atomicMax(&p.rowmax[s0 + q0 + qb + i], __float_as_uint(a[i]));
       }
     }
   }

@@ -55,6 +55,24 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // max(m, a) that ignores a NaN `a`, like `if a > max_abs { max_abs = a }`.
 __device__ __forceinline__ float nanless_max(float m, float a) { return a > m ? a : m; }
 
+// DPP lane permutations within rows of 16 lanes
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xF, 0xF, true);  // every lane has a source
+}
+
+// max over the 16 lanes of this lane's DPP row (every lane gets it)
+__device__ __forceinline__ float row16_max(float m) {
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor1>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor2>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(m))));
+  return fmaxf(m, __uint_as_float(dpp<kDppMirror>(__float_as_uint(m))));
+}
+
 // Orders this wave's LDS accesses before and after it (LDS data private to one
 // wave needs no workgroup barrier: a wave's LDS operations complete in order once
 // the counter is drained).

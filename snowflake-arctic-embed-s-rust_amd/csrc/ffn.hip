@@ -40,24 +40,6 @@ constexpr int kEPitch = kDnCB * 16 + 4;   // per-wave epilogue staging row pitch
 constexpr int kRing = 8;                  // FFN-down K steps of weight fragments in flight
 constexpr int kUpSteps = kH / 64, kDnSteps = kF / 64;
 
-// DPP lane permutations within rows of 16 lanes
-constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
-constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
-template <int kCtrl>
-__device__ __forceinline__ uint32_t dpp(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, kCtrl, 0xF, 0xF, true);  // every lane has a source
-}
-
-// max over the 16 lanes of this lane's DPP row (every lane gets it)
-__device__ __forceinline__ float row16_max(float m) {
-  m = fmaxf(m, __uint_as_float(dpp<kDppXor1>(__float_as_uint(m))));
-  m = fmaxf(m, __uint_as_float(dpp<kDppXor2>(__float_as_uint(m))));
-  m = fmaxf(m, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(m))));
-  return fmaxf(m, __uint_as_float(dpp<kDppMirror>(__float_as_uint(m))));
-}
-
 // 4 x 4 byte transpose over the lanes of a quad: lane k holds byte r = M[r][k]
 // (a column); afterwards it holds byte c = M[k][c] (a row).  Two exchanges
 // (lane k^1, then k^2), each followed by one byte select (v_perm_b32: selector
