@@ -26,12 +26,15 @@ namespace aek {
 // ---------------------------------------------------------------------------
 constexpr int kAttnQ = 32;     // queries per workgroup
 
-// Work plan, built on the device from cu_seqlens: plan[b] = sum_{b'<b}
-// ceil(L_b'/kAttnQ) (plan[B] = number of tiles) and, after it, tile_seg[tile] =
-// the segment of each tile, so a workgroup finds its segment with one load.
-// Tiles follow the packed segment order (neighbouring tiles read neighbouring
-// K/V rows).  Rows past lmax (the score row length) get no tiles.
-__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int* plan) {
+// Work plan, built on the device from cu_seqlens: one 16-byte record per tile
+// of kAttnQ queries, {s0, L, q0, nq} = the segment's first token, its length,
+// the tile's first query and its number of queries, so a workgroup learns its
+// whole assignment from one scalar load.  Tiles follow the packed segment order
+// (neighbouring tiles read neighbouring K/V rows); records past the last tile,
+// up to max_tiles, have nq = 0.  Rows past lmax (the score row length) get no
+// tiles.
+__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int max_tiles,
+                                                             int4* plan) {
   __shared__ int part[256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
@@ -47,17 +50,15 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
       part[i] = acc;
       acc += v;
     }
-    plan[B] = acc;
+    part[0] = acc;  // slot 0's own prefix is 0 (kept in `at` below)
   }
   __syncthreads();
-  int* tile_seg = plan + B + 1;
-  int at = part[tid];
+  int at = tid == 0 ? 0 : part[tid];
   for (int b = b0; b < b1; b++) {
-    plan[b] = at;
-    const int n = (min(cu[b + 1] - cu[b], lmax) + kAttnQ - 1) / kAttnQ;
-    for (int i = 0; i < n; i++) tile_seg[at + i] = b;
-    at += n;
+    const int s0 = cu[b], L = min(cu[b + 1] - s0, lmax);
+    for (int q0 = 0; q0 < L; q0 += kAttnQ) plan[at++] = make_int4(s0, L, q0, min(kAttnQ, L - q0));
   }
+  for (int t = part[0] + tid; t < max_tiles; t += 256) plan[t] = make_int4(0, 0, 0, 0);
 }
 
 // MFMA as an exact multiplier.  v_mfma_f32_16x16x1_4b_f32 with a zero
@@ -113,14 +114,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
   const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
   const int h = item / max_tiles, tile = item - h * max_tiles;
-  const int* tile_start = p.plan;
-  if (tile >= tile_start[p.B]) return;
-  const int b = tile_start[p.B + 1 + tile];  // tile_seg
-  const int s0 = p.cu[b];
+  const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
+  const int nq = rec.w;
+  if (nq == 0) return;
+  const int s0 = rec.x, L = rec.y, q0 = rec.z;  // L <= pitch - 4 (the plan clamps it)
   const int pitch = p.s_pitch;
-  const int L = min(p.cu[b + 1] - s0, pitch - 4);  // the host sizes pitch >= round16(L) + 4
-  const int q0 = (tile - tile_start[b]) * kAttnQ;
-  const int nq = min(kAttnQ, L - q0);
   const int nqh = (nq + 15) >> 4;  // query halves with at least one query
   float* S = smem;                 // [kAttnQ][pitch]
   const int tid = threadIdx.x, lane = tid & 63;
@@ -461,17 +459,20 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     // Lane l holds queries qb .. qb + 3 at dim d.  With `rowmax`, each query's
     // max |ctx * inv_smooth| over this wave's 16 dims (one DPP row; every value
     // is a non-NaN >= +0, where fmaxf is the reference's `if a > max` scan) goes
-    // to rowmax by atomicMax on its f32 bits.  All stores are issued last, with
-    // no wait between them.
+    // to rowmax by atomicMax on its f32 bits.  The maxima are formed before any
+    // store is issued (a wait for the inv_smooth load placed after the stores
+    // would also wait for them), and the stores go out last with no wait between.
     const int qb = 16 * qh + 4 * lg, d = 16 * dh + lr;
+    float a[4];
+    if (p.rowmax) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) a[i] = row16_max(nanless_max(0.0f, fabsf(acc[i] * sm)));
+    }
     float* out = p.ctx + (size_t)(s0 + q0 + qb) * H + h * 32 + d;
 #pragma unroll
     for (int i = 0; i < 4; i++)
       if (qb + i < nq) out[(size_t)i * H] = acc[i];
     if (p.rowmax) {
-      float a[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) a[i] = row16_max(nanless_max(0.0f, fabsf(acc[i] * sm)));
       if (lr == 0) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -655,8 +656,9 @@ void init_attention_kernels() {
 // batch's mean length (both variants give the same bits).
 constexpr int kWideMinMeanLen = 48;
 
-void launch_attention_plan(const AttnArgs& p, hipStream_t st) {
-  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4, p.plan);
+void launch_attention_plan(const AttnArgs& p, int T, hipStream_t st) {
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4,
+                     attention_max_tiles(p.B, T), reinterpret_cast<int4*>(p.plan));
 }
 
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
@@ -670,7 +672,7 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
     hipLaunchKernelGGL(attention_rows_kernel<4>, dim3(p.B * 12), dim3(256), 0, st, p);
     return;
   }
-  if (plan) launch_attention_plan(p, st);
+  if (plan) launch_attention_plan(p, T, st);
   const int max_tiles = attention_max_tiles(p.B, T);
   const size_t lds = attention_lds_bytes(p.s_pitch);
   if (T > kWideMinMeanLen * p.B)

@@ -97,7 +97,7 @@ struct AttnArgs {
   const float* qkv;        // [T,1152]
   const int* cu;           // [B+1]
   int B;
-  int* plan;               // scratch: attention_plan_ints(B, T) ints
+  int* plan;               // scratch: attention_plan_ints(B, T) ints, 16-byte aligned
   float* ctx;              // [T,384]
   const float* smooth;     // attn_out inv_smooth [384] or null
   uint32_t* rowmax;        // [T] or null
@@ -107,13 +107,13 @@ int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
 // tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32); T/32 + B + 1 is one
 inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
-// ints of `plan` scratch for B segments and T tokens: tile prefix [B+1] + tile_seg [max_tiles]
-inline size_t attention_plan_ints(int B, int T) { return (size_t)B + 1 + attention_max_tiles(B, T); }
+// ints of `plan` scratch for B segments and T tokens: one 4-int record per tile
+inline size_t attention_plan_ints(int B, int T) { return 4 * (size_t)attention_max_tiles(B, T); }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
 // T = total tokens of the batch; plan = false reuses the plan already in p.plan
-// (launch_attention_plan, which depends only on cu and B)
+// (launch_attention_plan, which depends only on cu, B, T and s_pitch)
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
-void launch_attention_plan(const AttnArgs& p, hipStream_t st);
+void launch_attention_plan(const AttnArgs& p, int T, hipStream_t st);
 // test hook: raw results of the exact-product MFMA (16 floats per lane per set of 64 pairs)
 void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st);
 
