@@ -58,6 +58,7 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   __shared__ __attribute__((aligned(16))) int8_t sA[2][kBM * kAPitch];
   __shared__ __attribute__((aligned(16))) int sE[4][16 * kEPitch];  // per-wave epilogue staging
   __shared__ uint32_t sRowMax[4][16];
+  __shared__ __attribute__((aligned(16))) float sEpSa[kBM], sEpWs[kBN], sEpB[kBN];  // epilogue operands
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // 1-D grid of (row tile, column tile) items.  p.col_fast: column tile fastest,
   // numbered XCD-contiguously, so the column tiles of one row tile run back to
@@ -90,6 +91,18 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   const int arow = min(m0 + lrow, p.M - 1);
   float a_inv = 0.0f;
   if (AM != kAI8) a_inv = 127.0f / __uint_as_float(p.a_rowmax[arow]);  // inv_scale = 127.0 / max_abs
+  // epilogue operands, loaded now and put in LDS after the K loop: thread t < kBM
+  // the scale of row m0 + t, then the w_scale and the bias float4s of the
+  // workgroup's kBN columns
+  float4 ep_reg = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (tid < kBM) {
+    const int r = min(m0 + tid, p.M - 1);
+    ep_reg.x = AM == kAI8 ? p.a_scale[r] : __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
+  } else if (tid < kBM + kBN / 4) {
+    ep_reg = reinterpret_cast<const float4*>(p.w_scale + n0)[tid - kBM];
+  } else if (tid < kBM + kBN / 2) {
+    ep_reg = reinterpret_cast<const float4*>(p.bias + n0)[tid - kBM - kBN / 4];
+  }
   auto aload = [&](int kt, ARegs<AM>& r) {
     const int kb = (KB + kt) * 64 + lpart * 16;
     if constexpr (AM == kAI8) {
@@ -191,6 +204,31 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
     }
     return;
   }
+  // Epilogue operands.  The row scales and the w_scale / bias columns of this
+  // workgroup, loaded at the start (ep_reg), are in LDS (sEp*) by now.  Lane
+  // (k, idx = lane + 64k) covers block row idx / kF4 and float4 column idx % kF4
+  // of every 16-row block; with f32 A (registers to spare once the K loop is
+  // done) the residual float4s of block i + 1 are loaded while block i is
+  // processed, otherwise each block loads its own.
+  constexpr bool kPre = AM != kAI8;
+  constexpr int kEk = kF4 / 4;  // float4s per lane and block
+  float4 resv[2][kPre ? kEk : 1];
+  auto load_res = [&](int i, int k) {
+    const int row = min(m0 + i * 16 + (lane + 64 * k) / kF4, p.M - 1);
+    const int col = col0 + ((lane + 64 * k) % kF4) * 4;
+    const v4i r4i = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.res + (size_t)row * p.N + col));
+    return make_float4(__int_as_float(r4i.x), __int_as_float(r4i.y), __int_as_float(r4i.z), __int_as_float(r4i.w));
+  };
+  if constexpr (kPre) {
+    if (p.res) {
+#pragma unroll
+      for (int k = 0; k < kEk; k++) resv[0][k] = load_res(0, k);
+    }
+  }
+  if (tid < kBM) sEpSa[tid] = ep_reg.x;
+  else if (tid < kBM + kBN / 4) reinterpret_cast<float4*>(sEpWs)[tid - kBM] = ep_reg;
+  else if (tid < kBM + kBN / 2) reinterpret_cast<float4*>(sEpB)[tid - kBM - kBN / 4] = ep_reg;
+  __syncthreads();
 #pragma unroll
   for (int i = 0; i < 4; i++) {
 #pragma unroll
@@ -199,22 +237,24 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
       for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
     if (EM == kEpiGelu && lane < 16) sRowMax[wave][lane] = 0u;
     wave_lds_sync();  // E and sRowMax are private to this wave
+    if constexpr (kPre) {
+      if (p.res && i + 1 < 4) {
 #pragma unroll
-    for (int k = 0; k < kF4 / 4; k++) {  // 16 rows x kF4 float4 over 64 lanes
+        for (int k = 0; k < kEk; k++) resv[(i + 1) & 1][k] = load_res(i + 1, k);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kEk; k++) {  // 16 rows x kF4 float4 over 64 lanes
       const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
       const int row = m0 + i * 16 + rr;
       const bool ok = row < p.M;
-      const int rrow = ok ? row : p.M - 1;
       const int col = col0 + c4 * 4;
-      float sa;
-      if (AM == kAI8) sa = p.a_scale[rrow];
-      else sa = __uint_as_float(p.a_rowmax[rrow]) / 127.0f;  // scale = max_abs / 127.0
       const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
-      const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
-      float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
+      const float sa = sEpSa[i * 16 + rr];
+      const float4 ws4 = *reinterpret_cast<const float4*>(&sEpWs[wave * kWaveN + c4 * 4]);
+      float4 b4 = *reinterpret_cast<const float4*>(&sEpB[wave * kWaveN + c4 * 4]);
       if (p.res) {
-        const v4i r4i = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.res + (size_t)rrow * p.N + col));
-        const float4 r4 = make_float4(__int_as_float(r4i.x), __int_as_float(r4i.y), __int_as_float(r4i.z), __int_as_float(r4i.w));
+        const float4 r4 = kPre ? resv[i & 1][kPre ? k : 0] : load_res(i, k);
         b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
       }
       float4 v;
