@@ -104,8 +104,8 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 //
 // kWide: operands in float4 groups with four MFMA results live at a time (one
 // float4 load of K per 16 dims, one float4 LDS read of P per 16 keys, and four
-// back-to-back MFMAs before their adds), ~146 VGPRs.  Otherwise one MFMA result
-// at a time with scalar operands, 80 VGPRs: for short rows, where the score
+// back-to-back MFMAs before their adds), 160 VGPRs.  Otherwise one MFMA result
+// at a time with scalar operands, 92 VGPRs: for short rows, where the score
 // tile leaves room for more waves than the wide variant's registers do.
 template <bool kWide>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles) {
