@@ -174,6 +174,15 @@ int ae_gelu_smooth_quantize(int m, int n, float* x_dev, const float* inv_smooth_
  * segments longer than 512 are cut to their first 512 rows. */
 int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
                         int total_tokens, float* ctx_dev, void* stream);
+/* The same attention as the reference's ArmSme backend computes it over a
+ * packed batch (attention_multihead_sme with segment ranges, src/model.rs:607-621,
+ * src/simd_math.rs:1933-2192): int8 Q and K per token and head, int8 V per head
+ * column over all total_tokens rows, integer scores, the exact-range int16
+ * softmax (round(16383 * 2^(s - max)), exp2 in log2 units) and integer P @ V.
+ * Bit-identical to that path; within a cosine budget of ae_attention_varlen.
+ * Same arguments and synchronization as ae_attention_varlen. */
+int ae_attention_varlen_quantized(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
+                                  int total_tokens, float* ctx_dev, void* stream);
 
 /* ---- tools and test hooks (no counterpart in the reference) -------------- */
 /* Writes a seeded synthetic model in `.ae8` layout (fp32

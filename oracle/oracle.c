@@ -725,3 +725,119 @@ int or_embed_batch_tokens_k(const or_model* m, const uint16_t* ids, const uint32
   }
   return atomic_load(&j.err);
 }
+
+
+/* ===========================================================================
+ * Quantized (ArmSme backend) attention, src/simd_math.rs:1933-2192 with the
+ * helpers it calls; see oracle.h.  NEON semantics restated per lane:
+ * vcvtnq_s32_f32 = round to nearest, ties to even (rintf in the default
+ * rounding mode), saturating to int32; vqmovn = saturating narrow; vfmaq_f32(a,
+ * b, c) = fmaf(b, c, a); vcvtmq_s32_f32 = floor to int32.
+ * ======================================================================== */
+static int32_t cvtn_s32(float x) {
+  if (x != x) return 0;
+  const float r = rintf(x);
+  if (r >= 2147483648.0f) return INT32_MAX;
+  if (r < -2147483648.0f) return INT32_MIN;
+  return (int32_t)r;
+}
+static int8_t sat_s8(int32_t v) { return (int8_t)(v > 127 ? 127 : (v < -128 ? -128 : v)); }
+static float fmax_nn(float a, float b) { return b > a ? b : a; } /* vmaxq on non-NaN data */
+
+int32_t or_exp2_q(float x, float scale, float x_min) {
+  /* src/simd_math.rs:2353-2370 */
+  x = x > x_min ? x : x_min; /* vmaxq_f32(x, x_min) */
+  const int32_t n = (int32_t)floorf(x);
+  const float f = x - (float)n;
+  float p = fmaf(f, 0.07842169f * scale, 0.22511937f * scale);
+  p = fmaf(f, p, 0.6963853f * scale);
+  p = fmaf(f, p, 0.999857f * scale);
+  uint32_t bits;
+  memcpy(&bits, &p, 4);
+  bits = (uint32_t)((int32_t)bits + (int32_t)((uint32_t)n << 23));
+  float scaled;
+  memcpy(&scaled, &bits, 4);
+  return cvtn_s32(scaled);
+}
+
+/* quantize_head32_row_neon (src/simd_math.rs:2482-2526): int8 row, returns the scale */
+static float sme_quant_row32(const float* src, float out_scale_mul, int8_t* q) {
+  float m = 0.0f;
+  for (int i = 0; i < 32; i++) m = fmax_nn(m, fabsf(src[i]));
+  const float max_abs = m > 1e-8f ? m : 1e-8f; /* f32::max(1e-8) */
+  const float inv_s = 127.0f / max_abs;
+  for (int i = 0; i < 32; i++) q[i] = sat_s8(cvtn_s32(src[i] * inv_s));
+  return (max_abs / 127.0f) * out_scale_mul;
+}
+
+void or_attention_sme(const float* qkv, int T, const int* cu, int B, float* ctx) {
+  const int HID = 384, STR = 3 * 384;
+  const float inv_sqrt_d = 1.0f / sqrtf(32.0f);
+  const float k_scale_mul = inv_sqrt_d * 1.44269504088896340736f; /* inv_sqrt_d * LOG2_E in f32 */
+  const float p_q16_max = 16383.0f;
+  int8_t* qi = (int8_t*)malloc((size_t)T * 32);
+  int8_t* ki = (int8_t*)malloc((size_t)T * 32);
+  int8_t* vi = (int8_t*)malloc((size_t)T * 32);
+  float* qs = (float*)malloc((size_t)T * 4);
+  float* ks = (float*)malloc((size_t)T * 4);
+  float* srow = (float*)malloc((size_t)T * 4);
+  int32_t* prow = (int32_t*)malloc((size_t)T * 4);
+  int* seg = (int*)malloc((size_t)T * sizeof(int));
+  for (int b = 0; b < B; b++)
+    for (int t = cu[b]; t < cu[b + 1]; t++) seg[t] = b;
+  for (int h = 0; h < 12; h++) {
+    const int ho = h * 32;
+    /* V: per-column max over all T tokens, scales, int8 (pack_qkv_head_int8_neon step 1) */
+    float vm[32], vscale[32], vinv[32];
+    for (int c = 0; c < 32; c++) vm[c] = 1e-8f;
+    for (int t = 0; t < T; t++)
+      for (int c = 0; c < 32; c++) vm[c] = fmax_nn(vm[c], fabsf(qkv[(size_t)t * STR + 2 * HID + ho + c]));
+    for (int c = 0; c < 32; c++) {
+      vscale[c] = vm[c] * (1.0f / 127.0f);
+      vinv[c] = 127.0f / vm[c];
+    }
+    for (int t = 0; t < T; t++)
+      for (int c = 0; c < 32; c++) vi[(size_t)t * 32 + c] = sat_s8(cvtn_s32(qkv[(size_t)t * STR + 2 * HID + ho + c] * vinv[c]));
+    /* Q, K: per-token int8 (step 2) */
+    for (int t = 0; t < T; t++) {
+      qs[t] = sme_quant_row32(qkv + (size_t)t * STR + ho, 1.0f, qi + (size_t)t * 32);
+      ks[t] = sme_quant_row32(qkv + (size_t)t * STR + HID + ho, k_scale_mul, ki + (size_t)t * 32);
+    }
+    for (int r = 0; r < T; r++) {
+      const int s0 = cu[seg[r]], s1 = cu[seg[r] + 1], len = s1 - s0;
+      /* raw scores and their dequantization: s = (f32(acc) * k_scale) * q_scale, log2 units */
+      float mx = -INFINITY;
+      const int nv = len & ~7; /* the NEON loop's 8-aligned part */
+      for (int j = 0; j < len; j++) {
+        int32_t acc = 0;
+        for (int i = 0; i < 32; i++) acc += (int32_t)qi[(size_t)r * 32 + i] * (int32_t)ki[(size_t)(s0 + j) * 32 + i];
+        const float v = ((float)acc * ks[s0 + j]) * qs[r];
+        srow[j] = v;
+        if (j < nv) mx = fmax_nn(mx, v);
+      }
+      for (int j = nv; j < len; j++)
+        if (srow[j] > mx) mx = srow[j];
+      /* exact-range int16 quantization and its integer sum */
+      int32_t isum = 0;
+      for (int j = 0; j < len; j++) {
+        int32_t q;
+        if (j < nv) {
+          q = or_exp2_q(srow[j] - mx, p_q16_max, -16.0f);
+        } else { /* ((s - max).exp2() * 16383).round() as i32, clamped */
+          const float e = roundf(exp2f(srow[j] - mx) * p_q16_max);
+          q = e != e ? 0 : (e >= 2147483648.0f ? INT32_MAX : (e < -2147483648.0f ? INT32_MIN : (int32_t)e));
+          q = q < 0 ? 0 : (q > 16383 ? 16383 : q);
+        }
+        isum += q;
+        prow[j] = q > 32767 ? 32767 : (q < -32768 ? -32768 : q); /* vqmovn to the i16 row */
+      }
+      const float p_scale = 1.0f / (float)(isum > 1 ? isum : 1);
+      for (int c = 0; c < 32; c++) {
+        int32_t acc = 0;
+        for (int j = 0; j < len; j++) acc += prow[j] * (int32_t)vi[(size_t)(s0 + j) * 32 + c];
+        ctx[(size_t)r * HID + ho + c] = (float)acc * (vscale[c] * p_scale);
+      }
+    }
+  }
+  free(qi); free(ki); free(vi); free(qs); free(ks); free(srow); free(prow); free(seg);
+}

@@ -121,6 +121,22 @@ void or_l2(float* v, int n);
 void or_attention_head(const float* qkv, int len, int stride, int q_off, int k_off,
                        int v_off, float* ctx, int ctx_stride);
 
+/* Quantized attention of the reference's ArmSme backend over a packed batch of T
+   tokens in B segments (cu[B+1]): attention_multihead_sme with seg_ranges
+   (src/model.rs:607-621; src/simd_math.rs:1933-2192), restated in scalar C:
+   per-token int8 Q and K (quantize_head32_row_neon, :2482-2526; K's scale also
+   carries log2(e)/sqrt(32)), per-column int8 V over all T tokens
+   (pack_qkv_head_int8_neon, :2564-2640; quantize_v_row_neon, :2530-2559),
+   integer scores, the two-pass exact-range int16 softmax per segment row
+   (softmax_quantize_i16_from_acc_neon, :2291-2336, with exp2_q_neon's
+   polynomial for 8-aligned chunks and exp2f for the row's last len % 8 keys,
+   :2353-2410), integer P @ V and ctx = f32(acc) * (v_scale * p_scale).
+   qkv: [T, 1152] f32; ctx: [T, 384] f32. */
+void or_attention_sme(const float* qkv, int T, const int* cu, int B, float* ctx);
+/* exp2_q_neon for one lane: round(scale * 2^x) for x <= 0, x clamped at x_min
+   (src/simd_math.rs:2353-2370) */
+int32_t or_exp2_q(float x, float scale, float x_min);
+
 /* ---- backend kernel table ------------------------------------------------
  * The drivers below (src/model.rs forward passes, src/lib.rs embed_batch) call
  * their row / GEMM / attention kernels through this table, as the reference

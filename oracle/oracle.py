@@ -68,6 +68,8 @@ _sigs = {
     "or_l2": (None, [_vp, ctypes.c_int]),
     "or_attention_head": (None, [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
                                  ctypes.c_int]),
+    "or_attention_sme": (None, [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp]),
+    "or_exp2_q": (ctypes.c_int32, [ctypes.c_float, ctypes.c_float, ctypes.c_float]),
     "or_forward_cls": (ctypes.c_int, [_MP, _vp, ctypes.c_size_t, _vp]),
     "or_forward_cls_unpruned": (ctypes.c_int, [_MP, _vp, ctypes.c_size_t, _vp]),
     "or_forward_ragged_cls": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, _vp]),
@@ -382,3 +384,19 @@ def attention(qkv, cu):
             _lib.or_attention_head(qkv[s0:].ctypes.data, L, 3 * H, h * 32, H + h * 32, 2 * H + h * 32,
                                    ctx[s0:, h * 32:].ctypes.data, H)
     return ctx
+
+
+def attention_sme(qkv, cu):
+    """The reference's quantized (ArmSme) attention over a packed batch
+    (src/model.rs:607-621, src/simd_math.rs:1933-2192)."""
+    qkv = _f32(qkv)
+    cu = np.ascontiguousarray(cu, np.int32)
+    T = qkv.shape[0]
+    ctx = np.zeros((T, H), np.float32)
+    _lib.or_attention_sme(qkv.ctypes.data, T, cu.ctypes.data, len(cu) - 1, ctx.ctypes.data)
+    return ctx
+
+
+def exp2_q(x, scale=16383.0, x_min=-16.0):
+    """exp2_q_neon for one lane (src/simd_math.rs:2353-2370)."""
+    return int(_lib.or_exp2_q(float(x), float(scale), float(x_min)))

@@ -65,6 +65,7 @@ _SIGS = {
     "ae_smooth_quantize": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ae_gelu_smooth_quantize": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ae_attention_varlen": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "ae_attention_varlen_quantized": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "ae_write_synthetic_ae8": (_i32, [_c.c_char_p, _u64]),
     "ae_tokenizer_open": (_i32, [_c.c_char_p, _c.POINTER(_vp)]),
     "ae_tokenizer_close": (None, [_vp]),
@@ -422,6 +423,11 @@ def gelu_smooth_quantize(m, n, x_ptr, smooth_ptr, q_ptr, scale_ptr, stream=None)
 
 def attention_varlen(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None):
     _check(_lib.ae_attention_varlen(qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), ctx_ptr, stream))
+
+
+def attention_varlen_quantized(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None):
+    """attention_varlen as the reference's ArmSme backend computes it (int8 Q/K/V, int16 P)."""
+    _check(_lib.ae_attention_varlen_quantized(qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), ctx_ptr, stream))
 
 
 def gelu_map(x_ptr, y_ptr, n, stream=None):

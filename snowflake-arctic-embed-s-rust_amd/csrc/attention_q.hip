@@ -1,0 +1,292 @@
+// attention_q.hip -- the reference's quantized attention (its ArmSme backend,
+// attention_multihead_sme with segment ranges: src/model.rs:607-621,
+// src/simd_math.rs:1933-2192), on int8 MFMA:
+//   Q, K: int8 per token and head (quantize_head32_row_neon, :2482-2526), K's
+//         scale also carrying log2(e)/sqrt(32);
+//   V:    int8 per head column over every token of the packed batch
+//         (pack_qkv_head_int8_neon, :2564-2640; quantize_v_row_neon, :2530-2559);
+//   s   = (f32(q.k) * k_scale) * q_scale   (log2 units);
+//   p   = round(16383 * 2^(s - max)) per segment row: exp2_q_neon's cubic for
+//         the row's 8-aligned part, glibc exp2f for its last len % 8 keys
+//         (softmax_quantize_i16_from_acc_neon / softmax_exp2_quantize_pass_i16_neon,
+//         :2291-2410), p_scale = 1 / max(sum p, 1);
+//   ctx = f32(sum_t p_t * v_t) * (v_scale * p_scale).
+// Every step is integer or one rounded f32 / f64 operation in the reference's
+// order, so the result is bit-identical to the reference's path on the same qkv.
+#include <hip/hip_runtime.h>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace aek {
+
+namespace {
+constexpr int kSmeQ = 32;  // queries per workgroup (the exact kernel's tile plan)
+typedef long v_i64;
+
+// vcvtnq_s32_f32 on in-range values: round to nearest, ties to even
+__device__ __forceinline__ int cvtn(float x) {
+  const float r = __builtin_rintf(x);
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));  // NaN -> 0
+  return q;
+}
+__device__ __forceinline__ int sat8(int v) { return min(127, max(-128, v)); }
+// f32::round (half away from zero), then `as i32` on an in-range value
+__device__ __forceinline__ int cvtn_away(float x) {
+  const float r = roundf(x);
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+  return q;
+}
+// vmaxq_f32 over non-NaN values
+__device__ __forceinline__ float vmax(float a, float b) { return b > a ? b : a; }
+
+// quantize_head32_row_neon over one 32-float row: int8 values into q (8-byte
+// aligned), returns (max_abs / 127) * mul
+__device__ __forceinline__ float quant_row32(const float* src, float mul, int8_t* q) {
+  float4 v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = reinterpret_cast<const float4*>(src)[i];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) m = vmax(vmax(vmax(vmax(m, fabsf(v[i].x)), fabsf(v[i].y)), fabsf(v[i].z)), fabsf(v[i].w));
+  const float max_abs = m > 1e-8f ? m : 1e-8f;
+  const float inv_s = 127.0f / max_abs;
+  uint32_t w[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    w[i] = pack4(sat8(cvtn(v[i].x * inv_s)), sat8(cvtn(v[i].y * inv_s)), sat8(cvtn(v[i].z * inv_s)),
+                 sat8(cvtn(v[i].w * inv_s)));
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    reinterpret_cast<uint4*>(q)[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  return (max_abs / 127.0f) * mul;
+}
+
+// exp2_q_neon (src/simd_math.rs:2353-2370) for one lane: round(scale * 2^x),
+// x clamped at x_min; the coefficients are f32 products with the scale, as the
+// reference forms them
+__device__ __forceinline__ int exp2_q16(float x) {
+  constexpr float S = 16383.0f;
+  x = vmax(x, -16.0f);
+  const float fl = floorf(x);
+  const int n = (int)fl;
+  const float f = x - fl;
+  float p = __builtin_fmaf(f, 0.07842169f * S, 0.22511937f * S);
+  p = __builtin_fmaf(f, p, 0.6963853f * S);
+  p = __builtin_fmaf(f, p, 0.999857f * S);
+  const float scaled = __int_as_float(__float_as_int(p) + (int)((uint32_t)n << 23));
+  return cvtn(scaled);
+}
+}  // namespace
+
+// Q and K of every token and head to int8 with their scales, and the per-column
+// |V| maximum over the batch folded into s.vmax (atomicMax on f32 bits; the
+// buffer is preset to bits(1e-8f), the reference's starting value).
+// 64 tokens per workgroup.
+__global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, SmeArgs s) {
+  const int tid = threadIdx.x, t0 = blockIdx.x * 64;
+  const float k_mul = kInvSqrtD * 1.44269504088896340736f;  // inv_sqrt_d * LOG2_E in f32
+  for (int it = tid; it < 64 * 12; it += 256) {
+    const int t = t0 + it / 12, h = it % 12;
+    if (t < T) {
+      const float* row = qkv + (size_t)t * HQKV + h * 32;
+      s.qs[t * 12 + h] = quant_row32(row, 1.0f, s.q8 + (size_t)t * H + h * 32);
+      s.ks[t * 12 + h] = quant_row32(row + H, k_mul, s.k8 + (size_t)t * H + h * 32);
+    }
+  }
+  for (int c = tid; c < H; c += 256) {
+    float m = 0.0f;
+    const int n = min(64, T - t0);
+    for (int i = 0; i < n; i++) m = vmax(m, fabsf(qkv[(size_t)(t0 + i) * HQKV + 2 * H + c]));
+    atomicMax(&s.vmax[c], __float_as_uint(m));
+  }
+}
+
+// One workgroup per (head, tile of 32 queries of one segment), the exact
+// kernel's tile records and XCD-contiguous numbering.  S[32][pitch] holds the
+// scores, then (in place, each element by the thread that read it) the int32
+// quantized probabilities.
+__global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ float s_maxw[4][kSmeQ];
+  __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32], s_vinv[32];
+  const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
+  const int h = item / max_tiles, tile = item - h * max_tiles;
+  const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
+  const int nq = rec.w;
+  if (nq == 0) return;
+  const int s0 = rec.x, L = rec.y, q0 = rec.z;
+  const int pitch = p.s_pitch;
+  float* S = smem;
+  int* Si = reinterpret_cast<int*>(smem);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const ExpTab tb = exp_tab_regs();
+  if (tid < 32) {
+    const float vm = __uint_as_float(sa.vmax[h * 32 + tid]);
+    s_vscale[tid] = vm * (1.0f / 127.0f);
+    s_vinv[tid] = 127.0f / vm;
+  }
+
+  // phase 1: integer scores, A = Q (16 queries x 32 dims), B = K (32 dims x 16
+  // keys), one v_mfma_i32_16x16x32_i8 per (key block, query half); lane l
+  // supplies row l % 16 and dims 8(l/16)..+7 of both, and ends with queries
+  // 4(l/16) + r of the half at key l % 16.  Rows past the segment are clamped
+  // (a clamped key repeats key L - 1's score, which cannot change the max).
+  const int nqh = (nq + 15) >> 4, nkb = (L + 15) >> 4;
+  v_i64 qa[2];
+  float qsc[2][4];
+#pragma unroll
+  for (int qh = 0; qh < 2; qh++) {
+    const int qrow = s0 + min(q0 + 16 * qh + lr, L - 1);
+    qa[qh] = *reinterpret_cast<const v_i64*>(sa.q8 + (size_t)qrow * H + h * 32 + 8 * lg);
+#pragma unroll
+    for (int r = 0; r < 4; r++) qsc[qh][r] = sa.qs[(s0 + min(q0 + 16 * qh + 4 * lg + r, L - 1)) * 12 + h];
+  }
+  float mrow[2][4];
+#pragma unroll
+  for (int qh = 0; qh < 2; qh++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) mrow[qh][r] = -INFINITY;
+  for (int kb = wave; kb < nkb; kb += 4) {  // wave-uniform
+    const int key = min(16 * kb + lr, L - 1);
+    const v_i64 kv = *reinterpret_cast<const v_i64*>(sa.k8 + (size_t)(s0 + key) * H + h * 32 + 8 * lg);
+    const float ksc = sa.ks[(s0 + key) * 12 + h];
+#pragma unroll
+    for (int qh = 0; qh < 2; qh++) {
+      if (qh >= nqh) break;  // wave-uniform
+      const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[qh], kv, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float sc = ((float)acc[r] * ksc) * qsc[qh][r];
+        S[(16 * qh + 4 * lg + r) * pitch + 16 * kb + lr] = sc;  // 16kb + lr < round16(L) <= pitch - 4
+        mrow[qh][r] = vmax(mrow[qh][r], sc);
+      }
+    }
+  }
+#pragma unroll
+  for (int qh = 0; qh < 2; qh++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float m = row16_max(mrow[qh][r]);  // non-NaN scores; -inf where a wave had no block
+      if (lr == 0) s_maxw[wave][16 * qh + 4 * lg + r] = m;
+    }
+  __syncthreads();
+  if (tid < kSmeQ) s_max[tid] = fmaxf(fmaxf(s_maxw[0][tid], s_maxw[1][tid]), fmaxf(s_maxw[2][tid], s_maxw[3][tid]));
+  __syncthreads();
+
+  // phase 2: p = round(16383 * 2^(s - max)) in place, 8 lanes per row (row
+  // tid / 8): the cubic over the first nv = L & ~7 keys, glibc exp2f over the
+  // last L - nv; the integer row sum is order-free.
+  {
+    const int row = tid >> 3, sub = tid & 7, nv = L & ~7;
+    const float m = s_max[row];
+    int* prow = Si + row * pitch;
+    const float* srow = S + row * pitch;
+    int isum = 0;
+    const bool live = row < nq;  // rows past the tile's queries hold no scores
+    for (int j = sub; j < nv; j += 8) {
+      const int q = exp2_q16(live ? srow[j] - m : -16.0f);
+      prow[j] = q;
+      isum += q;
+    }
+    {  // every lane evaluates (exp2f_libm needs the whole wave); lanes past L discard
+      const int j = nv + sub;
+      const bool in = live && j < L;
+      const float e = exp2f_libm(in ? srow[j] - m : 0.0f, tb);
+      int q = cvtn_away(e * 16383.0f);
+      q = min(16383, max(0, q));
+      if (in) {
+        prow[j] = q;
+        isum += q;
+      }
+    }
+    isum += __shfl_xor(isum, 1, 64);
+    isum += __shfl_xor(isum, 2, 64);
+    isum += __shfl_xor(isum, 4, 64);
+    if (sub == 0) s_pscale[row] = 1.0f / (float)max(isum, 1);
+  }
+  __syncthreads();
+
+  // phase 3: ctx = P @ V over chunks of 32 keys.  Wave w owns the 16 x 16
+  // (query, dim) quadrant (w / 2, w % 2).  p < 2^14 is split as 128 p_hi + p_lo
+  // (both in [0, 127]) so the int8 MFMA takes it; V is quantized on load.  The
+  // integer sums are exact, so ctx = f32(128 acc_hi + acc_lo) * (v_scale * p_scale).
+  const int qh = wave >> 1, dh = wave & 1;
+  if (qh < nqh) {
+    const int c = 16 * dh + lr;
+    const float vinv = s_vinv[c];
+    const int* prow = Si + (16 * qh + lr) * pitch;
+    const float* vcol = p.qkv + (size_t)s0 * HQKV + 2 * H + h * 32 + c;
+    v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+    for (int t0 = 0; t0 < L; t0 += 32) {  // wave-uniform
+      const int tb8 = t0 + 8 * lg;  // this lane's 8 keys
+      int pv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (tb8 < L) {  // reads stay below round8(L) <= pitch - 4
+        const int4 a = reinterpret_cast<const int4*>(prow + tb8)[0];
+        const int4 b = reinterpret_cast<const int4*>(prow + tb8)[1];
+        pv[0] = a.x; pv[1] = a.y; pv[2] = a.z; pv[3] = a.w;
+        pv[4] = b.x; pv[5] = b.y; pv[6] = b.z; pv[7] = b.w;
+      }
+      uint32_t hi[2], lo[2], vb[2];
+#pragma unroll
+      for (int w2 = 0; w2 < 2; w2++) {
+        int ph[4], pl[4], vq[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int k = 4 * w2 + i, t = tb8 + k;
+          const int pk = t < L ? pv[k] : 0;
+          ph[i] = pk >> 7;
+          pl[i] = pk & 127;
+          const float v = vcol[(size_t)min(t, L - 1) * HQKV];
+          vq[i] = t < L ? sat8(cvtn(v * vinv)) : 0;
+        }
+        hi[w2] = pack4(ph[0], ph[1], ph[2], ph[3]);
+        lo[w2] = pack4(pl[0], pl[1], pl[2], pl[3]);
+        vb[w2] = pack4(vq[0], vq[1], vq[2], vq[3]);
+      }
+      const v_i64 ah = (v_i64)(((uint64_t)hi[1] << 32) | hi[0]);
+      const v_i64 al = (v_i64)(((uint64_t)lo[1] << 32) | lo[0]);
+      const v_i64 bv = (v_i64)(((uint64_t)vb[1] << 32) | vb[0]);
+      acc_hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bv, acc_hi, 0, 0, 0);
+      acc_lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bv, acc_lo, 0, 0, 0);
+    }
+    const int qb = 16 * qh + 4 * lg;
+    const float vsc = s_vscale[c];
+    const float sm = p.rowmax ? p.smooth[h * 32 + c] : 0.0f;
+    float out[4], a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      out[i] = (float)(acc_hi[i] * 128 + acc_lo[i]) * (vsc * s_pscale[qb + i]);
+      a[i] = p.rowmax ? row16_max(nanless_max(0.0f, fabsf(out[i] * sm))) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (qb + i < nq) p.ctx[(size_t)(s0 + q0 + qb + i) * H + h * 32 + c] = out[i];
+    if (p.rowmax && lr == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (qb + i < nq) atomicMax(&p.rowmax[s0 + q0 + qb + i], __float_as_uint(a[i]));
+    }
+  }
+}
+
+void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan) {
+  if (T <= 0 || p.B <= 0) return;
+  launch_fill_u32(s.vmax, H, 0x322bcc77u, st);  // bits of 1e-8f
+  hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(256), 0, st, p.qkv, T, s);
+  if (plan) launch_attention_plan(p, T, st);
+  const int max_tiles = attention_max_tiles(p.B, T);
+  hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p, s,
+                     max_tiles);
+}
+
+void init_attention_sme_kernels() {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sme_attention_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_lds_bytes(attention_pitch(512)));
+}
+
+}  // namespace aek

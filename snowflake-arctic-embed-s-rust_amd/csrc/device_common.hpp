@@ -150,6 +150,30 @@ __device__ __forceinline__ float expf_libm(float x, const ExpTab& tb) {
   return x < -0x1.9fe368p6f ? 0.0f : res;  // glibc's underflow branch
 }
 
+// exp2f as glibc computes it (sysdeps/ieee754/flt-32/e_exp2f.c: the same
+// 32-entry table and cubic as expf_libm, unscaled coefficients, r = x - k/32 in
+// double, the -mfma build's contractions), for x <= 0 and NaN; x <= -150 gives
+// +0 as glibc's underflow branch does.  Wave-uniform control flow required
+// (see ExpTab).
+__device__ __forceinline__ float exp2f_libm(float x, const ExpTab& tb) {
+  const double kShift = 0x1.8p+52 / 32.0;
+  const double c0 = 0x1.c6af84b912394p-5, c1 = 0x1.ebfce50fac4f3p-3, c2 = 0x1.62e42ff0c52d6p-1;
+  const double xd = (double)x;
+  double kd = xd + kShift;
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= kShift;
+  const double r = xd - kd;
+  const uint64_t t = exp_tab_lookup(tb, (uint32_t)ki) + (ki << 47);
+  const double s = __longlong_as_double((long long)t);
+  const double z = __builtin_fma(c0, r, c1);
+  const double r2 = r * r;
+  double y = __builtin_fma(c2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  const float res = (float)y;
+  return x <= -150.0f ? 0.0f : res;
+}
+
 // scalar_gelu (reference src/simd_math.rs:15-23), same operation order.
 // Wave-uniform control flow required (see ExpTab).
 //

@@ -867,8 +867,21 @@ int ae_gelu_smooth_quantize(int m, int n, float* x_dev, const float* inv_smooth_
   return AE_OK;
 }
 
+static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                            float* ctx_dev, void* stream, bool quantized);
+
 int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
                         float* ctx_dev, void* stream) {
+  return attention_varlen(qkv_dev, cu_seqlens_dev, n_seqs, total_tokens, ctx_dev, stream, false);
+}
+
+int ae_attention_varlen_quantized(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                                  float* ctx_dev, void* stream) {
+  return attention_varlen(qkv_dev, cu_seqlens_dev, n_seqs, total_tokens, ctx_dev, stream, true);
+}
+
+static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                            float* ctx_dev, void* stream, bool quantized) {
   if (!qkv_dev || !cu_seqlens_dev || !ctx_dev || n_seqs < 0 || total_tokens < 0)
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
   if (n_seqs == 0) return AE_OK;
@@ -888,9 +901,26 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
   aek::init_attention_kernels();
   aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr,
                   aek::attention_pitch(std::min(max_len, ae::kMaxPos))};
-  aek::launch_attention(a, total_tokens, as_stream(stream));
+  void* sme = nullptr;
+  if (quantized) {  // int8 Q, K [T,384] each, their scales [T,12] each, the |V| column max [384]
+    const size_t T = size_t(total_tokens);
+    hipError_t e = hipMalloc(&sme, T * 384 * 2 + T * 12 * 4 * 2 + 384 * 4);
+    if (e != hipSuccess) {
+      (void)hipFree(plan);
+      return fail(AE_ERR_HIP, std::string("attention scratch: ") + hipGetErrorString(e));
+    }
+    char* b = static_cast<char*>(sme);
+    aek::SmeArgs sa{reinterpret_cast<int8_t*>(b), reinterpret_cast<int8_t*>(b + T * 384),
+                    reinterpret_cast<float*>(b + T * 768), reinterpret_cast<float*>(b + T * 768 + T * 48),
+                    reinterpret_cast<uint32_t*>(b + T * 768 + T * 96)};
+    aek::init_attention_sme_kernels();
+    aek::launch_attention_sme(a, sa, total_tokens, as_stream(stream));
+  } else {
+    aek::launch_attention(a, total_tokens, as_stream(stream));
+  }
   hipError_t err = hipStreamSynchronize(as_stream(stream));
   (void)hipFree(plan);
+  if (sme) (void)hipFree(sme);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));
   return AE_OK;
 }

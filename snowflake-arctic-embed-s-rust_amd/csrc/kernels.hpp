@@ -114,6 +114,18 @@ void init_attention_kernels();  // once per device before the first launch (not 
 // (launch_attention_plan, which depends only on cu, B, T and s_pitch)
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
 void launch_attention_plan(const AttnArgs& p, int T, hipStream_t st);
+// Quantized attention (the reference's ArmSme backend): scratch for the int8 Q
+// and K of every token and head, their scales and the per-column |V| maximum.
+struct SmeArgs {
+  int8_t* q8;       // [T,384]
+  int8_t* k8;       // [T,384]
+  float* qs;        // [T,12]
+  float* ks;        // [T,12]
+  uint32_t* vmax;   // [384], f32 bits
+};
+// the packing, the plan (plan = true) and the attention; p.smooth / p.rowmax as launch_attention
+void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan = true);
+void init_attention_sme_kernels();  // once per device before the first launch
 // test hook: raw results of the exact-product MFMA (16 floats per lane per set of 64 pairs)
 void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st);
 

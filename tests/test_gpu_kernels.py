@@ -266,6 +266,28 @@ def test_attention_bit_exact(torch_gpu, lens):
     assert np.array_equal(bits(ctx_d.cpu().numpy()), bits(ref))
 
 
+@pytest.mark.parametrize("lens", [[1, 2, 7, 8, 9, 15, 16, 17, 31, 32, 33], [5, 40, 97, 300, 1, 512, 63],
+                                  [100] * 3, [21, 3, 500]], ids=["edges", "ragged", "uniform", "long"])
+def test_attention_quantized_bit_exact(torch_gpu, lens):
+    """The reference's quantized (ArmSme) attention over a packed batch: int8 Q, K, V,
+    exact-range int16 P (the cubic on each row's 8-aligned part, exp2f on the rest):
+    bit-exact with the oracle."""
+    torch = torch_gpu
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    rng = np.random.default_rng(23)
+    qkv = rng.normal(0, 1.0, (T, 1152)).astype(f32)
+    qkv[:, 768:] *= rng.uniform(0.1, 3.0, 384).astype(f32)  # per-column V ranges
+    qkv_d, cu_d = dev(torch, qkv), dev(torch, cu)
+    ctx_d = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+    print("quantized attention lens", lens, flush=True)
+    ae.attention_varlen_quantized(qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, ctx_d.data_ptr())
+    torch.cuda.synchronize()
+    ref = orc.attention_sme(qkv, cu)
+    got = ctx_d.cpu().numpy()
+    assert np.array_equal(bits(got), bits(ref)), np.abs(got - ref).max()
+
+
 def test_mfma_products_equal_rounded_products(torch_gpu):
     """The attention kernels take every product from v_mfma_f32_16x16x1_4b_f32 with a zero
     accumulator: each result must be the correctly rounded f32 product (numpy's), including

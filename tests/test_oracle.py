@@ -325,3 +325,69 @@ def test_x86_backend_tracks_scalar_backend(oracle_model):
     cos = (ref.astype(np.float64) * got).sum(1) / (np.linalg.norm(ref, axis=1) * np.linalg.norm(got, axis=1))
     assert cos.min() > 0.999, cos
     assert np.allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+
+
+# ---- the reference's quantized (ArmSme) attention, src/simd_math.rs:1933-2410 ----
+
+def test_exp2_q_error_bound_and_endpoints():
+    """exp2_q_neon's cubic: within its documented 1.4e-4 relative error of
+    16383 * 2^x (plus the final rounding) on [-16, 0]; x = 0 gives round(0.999857 *
+    16383) = 16381, and x is clamped at -16 (16383 * 2^-16 = 0.25 -> 0)."""
+    xs = np.linspace(-16.0, 0.0, 20001, dtype=np.float32)
+    got = np.array([orc.exp2_q(x) for x in xs], np.float64)
+    ref = 16383.0 * np.exp2(xs.astype(np.float64))
+    assert np.all(np.abs(got - ref) <= 1.4e-4 * ref + 0.5 + 1e-9)
+    assert orc.exp2_q(0.0) == 16381
+    assert orc.exp2_q(-16.0) == 0 and orc.exp2_q(-40.0) == 0 and orc.exp2_q(-1e30) == 0
+    # monotone over the grid
+    assert np.all(np.diff(got) >= 0)
+
+
+def _qkv(T, seed):
+    return np.random.default_rng(seed).normal(0, 1.0, (T, 1152)).astype(np.float32)
+
+
+def test_attention_sme_single_key_returns_the_quantized_value_row():
+    """A one-token segment attends to itself with p = 16383 (exp2f tail, x = 0):
+    ctx = f32(16383 * v_q) * (v_scale / 16383), i.e. the dequantized V row, within
+    one quantization step of V."""
+    qkv = _qkv(40, 3)
+    cu = np.array([0, 1, 40], np.int32)
+    ctx = orc.attention_sme(qkv, cu)
+    v = qkv[0, 768:]
+    vmax = np.maximum(np.abs(qkv[:, 768:]).max(0), 1e-8)
+    assert np.all(np.abs(ctx[0] - v) <= vmax / 127.0 * 0.5 + 1e-6)
+
+
+def test_attention_sme_uniform_scores_average_v():
+    """Identical keys give identical scores, so every p equals 16381 (the cubic at
+    x = 0) or 16383 (the exp2f tail) and ctx is a near-uniform average of the
+    quantized V rows."""
+    T = 21  # 16 keys in the 8-aligned part, a 5-key tail
+    qkv = _qkv(T, 5)
+    qkv[:, 384:768] = qkv[0, 384:768]
+    cu = np.array([0, T], np.int32)
+    ctx = orc.attention_sme(qkv, cu)
+    f32 = np.float32
+    vmax = np.maximum(np.abs(qkv[:, 768:]).max(0), f32(1e-8)).astype(f32)
+    vq = np.clip(np.rint(qkv[:, 768:] * (f32(127.0) / vmax)), -128, 127).astype(np.int64)
+    w = np.array([16381] * 16 + [16383] * 5, np.int64)  # 8-aligned part, then the exp2f tail
+    acc = (w[:, None] * vq).sum(0)
+    ref = acc.astype(f32) * (vmax * f32(1.0 / 127.0) * (f32(1.0) / f32(w.sum())))
+    assert np.array_equal(ctx, np.broadcast_to(ref, ctx.shape))
+
+
+def test_attention_sme_close_to_exact_attention():
+    """The quantized path stays within a cosine budget of the exact attention
+    (the reference documents ~0.0009 of cosine lost with 7-bit P on long rows;
+    int16 P keeps the loss well below that)."""
+    lens = [5, 40, 97, 300, 1, 8, 9, 16, 17]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv = _qkv(int(cu[-1]), 7)
+    ex = orc.attention(qkv, cu).astype(np.float64)
+    qa = orc.attention_sme(qkv, cu).astype(np.float64)
+    for h in range(12):
+        a, b = ex[:, h * 32:(h + 1) * 32], qa[:, h * 32:(h + 1) * 32]
+        cos = (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+        assert cos.min() > 0.995, (h, cos.min())
+        assert np.median(cos) > 0.9995, (h, np.median(cos))
