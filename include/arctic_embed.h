@@ -209,6 +209,16 @@ int ae_workspace_set_timing(ae_workspace* ws, int enabled);
  * the same buffers, stream and batch shape captures the pass into a hipGraph and
  * later calls replay it.  Disabled while timing is on.  0 forces eager launches. */
 int ae_workspace_set_graphs(ae_workspace* ws, int enabled);
+/* Attention of layers 0-10 in this workspace's forward passes.
+ * AE_ATTENTION_EXACT (default): the reference's scalar order, bit-exact.
+ * AE_ATTENTION_QUANTIZED: what the reference's ArmSme backend computes
+ * (SimdBackend::ArmSme in src/model.rs:591-621 and :223-247: int8 Q, K, V and
+ * int16 P, see ae_attention_varlen_quantized) for batches of at least 32 packed
+ * tokens, or 16 for a single sequence; smaller batches keep the exact path.
+ * Setting it the first time allocates the mode's scratch for max_tokens rows. */
+#define AE_ATTENTION_EXACT 0
+#define AE_ATTENTION_QUANTIZED 1
+int ae_workspace_set_attention_mode(ae_workspace* ws, int mode);
 int ae_workspace_kernel_times(ae_workspace* ws, double* ms_out, int* counts);
 /* The fused GEMM variants of the forward pass, exposed for parity tests:
  * A given as f32 rows quantized on load with q = round((x*s_k)*(127/rowmax[m]))

@@ -374,6 +374,7 @@ typedef struct {
   int T, B;
   const int* seg_start; /* [B] */
   const int* seg_len;   /* [B] */
+  int sme;              /* attention of the reference's ArmSme backend (or_attention_sme) */
   float *hidden, *tmp, *qkv, *ctx, *inter;
   int8_t *act_q, *inter_q;
   float* act_scale;
@@ -402,12 +403,20 @@ static void full_layer(const or_model* m, int l, fwd_ws* w, int quant_next, cons
   const or_layer* L = &m->layers[l];
   const int T = w->T;
   K->gemm(T, w->act_q, w->act_scale, &L->qkv, NULL, w->qkv);
-  for (int b = 0; b < w->B; b++)
-    for (int h = 0; h < OR_HEADS; h++) {
-      const int ho = h * 32;
-      attention_head_k(w->qkv + (size_t)w->seg_start[b] * 3 * H, w->seg_len[b], 3 * H, ho, H + ho,
-                       2 * H + ho, w->ctx + (size_t)w->seg_start[b] * H + ho, H, K);
-    }
+  if (w->sme && T >= (w->B == 1 ? 16 : 32)) { /* src/model.rs:607-621 (:245 for one sequence) */
+    int* cu = (int*)malloc(sizeof(int) * (w->B + 1));
+    for (int b = 0; b < w->B; b++) cu[b] = w->seg_start[b];
+    cu[w->B] = T;
+    or_attention_sme(w->qkv, T, cu, w->B, w->ctx);
+    free(cu);
+  } else {
+    for (int b = 0; b < w->B; b++)
+      for (int h = 0; h < OR_HEADS; h++) {
+        const int ho = h * 32;
+        attention_head_k(w->qkv + (size_t)w->seg_start[b] * 3 * H, w->seg_len[b], 3 * H, ho, H + ho,
+                         2 * H + ho, w->ctx + (size_t)w->seg_start[b] * H + ho, H, K);
+      }
+  }
   for (int t = 0; t < T; t++)
     w->act_scale[t] = K->smooth_quant_row(w->ctx + (size_t)t * H, L->attn_out.inv_smooth,
                                           w->act_q + (size_t)t * H, H);
@@ -603,8 +612,21 @@ int or_forward_ragged_cls(const or_model* m, const uint16_t* ids, const uint32_t
   return forward_ragged_cls_k(m, ids, offsets, b, out, &or_scalar_kernels);
 }
 
+static int run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b, int upto_layer,
+                      float* hidden, int8_t* act_q, float* act_scale, int sme);
+
 int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
                   int upto_layer, float* hidden, int8_t* act_q, float* act_scale) {
+  return run_prefix(m, ids, offsets, b, upto_layer, hidden, act_q, act_scale, 0);
+}
+
+int or_run_prefix_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
+                      int upto_layer, float* hidden, int8_t* act_q, float* act_scale) {
+  return run_prefix(m, ids, offsets, b, upto_layer, hidden, act_q, act_scale, 1);
+}
+
+static int run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b, int upto_layer,
+                      float* hidden, int8_t* act_q, float* act_scale, int sme) {
   if (b < 1 || upto_layer < 0 || upto_layer > OR_LAYERS - 1) return OR_ERR_ARG;
   const uint16_t** seqs = (const uint16_t**)malloc(sizeof(void*) * b);
   int* lens = (int*)malloc(sizeof(int) * b);
@@ -620,7 +642,7 @@ int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offset
     T += len;
   }
   fwd_ws w = {0};
-  w.T = T; w.B = b; w.seg_start = starts; w.seg_len = lens;
+  w.T = T; w.B = b; w.seg_start = starts; w.seg_len = lens; w.sme = sme;
   fwd_alloc(&w, T);
   embed_tokens(m, seqs, &w, &or_scalar_kernels);
   for (int l = 0; l < upto_layer; l++) full_layer(m, l, &w, 1, &or_scalar_kernels);

@@ -185,6 +185,10 @@ int or_embed_batch_tokens(const or_model* m, const uint16_t* ids, const uint32_t
    and layers [0, upto_layer) and returns hidden/act_q/act_scale at that point. */
 int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
                   int upto_layer, float* hidden, int8_t* act_q, float* act_scale);
+/* or_run_prefix with the ArmSme backend's quantized attention in layers 0-10
+   (or_attention_sme for >= 32 packed tokens, >= 16 for one sequence) */
+int or_run_prefix_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
+                      int upto_layer, float* hidden, int8_t* act_q, float* act_scale);
 
 #ifdef __cplusplus
 }

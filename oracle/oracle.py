@@ -79,6 +79,7 @@ _sigs = {
     "or_x86_prepare": (ctypes.c_int, [_MP]),
     "or_x86_embed_batch_tokens": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
     "or_run_prefix": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
+    "or_run_prefix_sme": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(_lib, _n)
@@ -236,14 +237,19 @@ class OracleModel:
             raise ValueError("or_x86_embed_batch_tokens: %d" % rc)
         return out
 
-    def run_prefix(self, seqs, upto_layer):
+    def run_prefix_sme(self, seqs, upto_layer):
+        """run_prefix with the ArmSme backend's quantized attention in layers 0-10."""
+        return self.run_prefix(seqs, upto_layer, sme=True)
+
+    def run_prefix(self, seqs, upto_layer, sme=False):
         ids, offs = _pack(seqs)
         T = int(offs[-1])
         hidden = np.zeros((T, H), np.float32)
         act_q = np.zeros((T, H), np.int8)
         scale = np.zeros(T, np.float32)
-        rc = _lib.or_run_prefix(self._m, ids.ctypes.data, offs.ctypes.data, len(seqs), int(upto_layer),
-                                hidden.ctypes.data, act_q.ctypes.data, scale.ctypes.data)
+        fn = _lib.or_run_prefix_sme if sme else _lib.or_run_prefix
+        rc = fn(self._m, ids.ctypes.data, offs.ctypes.data, len(seqs), int(upto_layer),
+                hidden.ctypes.data, act_q.ctypes.data, scale.ctypes.data)
         if rc:
             raise ValueError("or_run_prefix: %d" % rc)
         return hidden, act_q, scale

@@ -75,6 +75,7 @@ _SIGS = {
     "ae_debug_mfma_products": (_i32, [_vp, _vp, _vp, ctypes.c_int, _vp]),
     "ae_workspace_set_timing": (_i32, [_vp, _i32]),
     "ae_workspace_set_graphs": (_i32, [_vp, _i32]),
+    "ae_workspace_set_attention_mode": (_i32, [_vp, _i32]),
     "ae_debug_forward_prefix": (_i32, [_vp, _vp, _vp, _vp, _sz, _i32, _vp, _vp, _vp]),
     "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
     "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -319,6 +320,10 @@ class Workspace:
     def set_graphs(self, enabled):
         """Graph replay of repeated forward passes (on by default); False forces eager launches."""
         _check(_lib.ae_workspace_set_graphs(self._h, 1 if enabled else 0))
+
+    def set_attention_mode(self, quantized):
+        """Layers 0-10 with the reference's ArmSme quantized attention (True) or the exact path."""
+        _check(_lib.ae_workspace_set_attention_mode(self._h, 1 if quantized else 0))
 
     def kernel_times(self):
         """{kind: (total_ms, launches)} since timing was enabled (synchronize first)."""

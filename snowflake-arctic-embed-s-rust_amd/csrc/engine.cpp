@@ -142,6 +142,10 @@ struct ae_workspace {
   uint16_t* ids = nullptr;
   int* cu = nullptr;
   int* attn_plan = nullptr;  // attention work plan, attention_plan_ints(max_seqs, max_tokens)
+  // AE_ATTENTION_QUANTIZED (ae_workspace_set_attention_mode): the reference's
+  // ArmSme attention in layers 0-10; its scratch is allocated when the mode is set
+  int attention_mode = AE_ATTENTION_EXACT;
+  aek::SmeArgs sme{};
   int* splitk = nullptr;     // int32 partial sums of split-K GEMMs (small M)
   size_t splitk_ints = 0;
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
@@ -169,8 +173,10 @@ struct ae_workspace {
     const void *ids, *cu, *out;
     hipStream_t st;
     int B, T, max_len;
+    int attention_mode;
     bool operator==(const GraphKey& o) const {
-      return ids == o.ids && cu == o.cu && out == o.out && st == o.st && B == o.B && T == o.T && max_len == o.max_len;
+      return ids == o.ids && cu == o.cu && out == o.out && st == o.st && B == o.B && T == o.T && max_len == o.max_len &&
+             attention_mode == o.attention_mode;
     }
   };
   struct GraphEntry {
@@ -390,6 +396,9 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     launch_ln_quant(p, kLnSrcEmb, st);
   }
   const int s_pitch = attention_pitch(max_len);
+  // the reference's ArmSme backend takes its quantized attention from 32 packed
+  // tokens on (src/model.rs:608), or 16 for a single sequence (:245)
+  const bool sme = ws->attention_mode == AE_ATTENTION_QUANTIZED && T >= (B == 1 ? 16 : 32);
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
     const DevLayer& D = E->layers[l];
@@ -400,7 +409,10 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
-      launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
+      if (sme)
+        launch_attention_sme(a, ws->sme, T, st, /*plan=*/l == 0);
+      else
+        launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
     }
     gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1,
                  gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
@@ -487,7 +499,7 @@ int run_forward_replay(ae_workspace* ws, const uint16_t* ids, const int* cu, int
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
     return run_forward(ws, ids, cu, B, T, max_len, out, st);
-  const ae_workspace::GraphKey key{ids, cu, out, st, B, T, max_len};
+  const ae_workspace::GraphKey key{ids, cu, out, st, B, T, max_len, ws->attention_mode};
   ws->graph_tick++;
   ae_workspace::GraphEntry* hit = nullptr;
   for (auto& g : ws->graph_cache)
@@ -958,6 +970,28 @@ int ae_write_synthetic_ae8(const char* path, uint64_t seed) {
   if (!path) return fail(AE_ERR_INVALID_ARG, "null path");
   std::string err;
   if (int rc = ae::write_synthetic_ae8(path, seed, err)) return fail(rc, err);
+  return AE_OK;
+}
+
+int ae_workspace_set_attention_mode(ae_workspace* ws, int mode) {
+  if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
+  if (mode != AE_ATTENTION_EXACT && mode != AE_ATTENTION_QUANTIZED)
+    return fail(AE_ERR_INVALID_ARG, "unknown attention mode");
+  if (mode == AE_ATTENTION_QUANTIZED && !ws->sme.vmax) {
+    HIP_TRY(hipSetDevice(ws->e->device));
+    const size_t T = size_t(ws->max_tokens);
+    int rc;
+    if ((rc = dalloc(&ws->sme.q8, T * 384)) || (rc = dalloc(&ws->sme.k8, T * 384)) || (rc = dalloc(&ws->sme.qs, T * 12)) ||
+        (rc = dalloc(&ws->sme.ks, T * 12)) || (rc = dalloc(&ws->sme.vmax, size_t(384))))
+      return rc;
+    ws->dev.push_back(ws->sme.q8);
+    ws->dev.push_back(ws->sme.k8);
+    ws->dev.push_back(ws->sme.qs);
+    ws->dev.push_back(ws->sme.ks);
+    ws->dev.push_back(ws->sme.vmax);
+    aek::init_attention_sme_kernels();
+  }
+  ws->attention_mode = mode;
   return AE_OK;
 }
 

@@ -232,3 +232,27 @@ def test_graph_replay_matches_eager(engine, oracle_model, torch_gpu):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), eager.view(np.uint32)), i
         engine.embed_batch_tokens(ws, other)  # other shapes through the same workspace in between
     ws.close()
+
+
+@pytest.fixture(scope="module")
+def ws_quant(engine):
+    w = engine.workspace(8192, 64)
+    w.set_attention_mode(True)
+    yield w
+    w.close()
+
+
+@pytest.mark.parametrize("case", ["ragged_l1", "ragged_l11", "single16", "single_short", "fused_ffn"])
+def test_quantized_attention_mode_prefix_state(engine, ws_quant, oracle_model, case):
+    """Workspace in AE_ATTENTION_QUANTIZED mode: the state after the embedding and
+    `layers` layers equals the oracle run with the ArmSme backend's attention in
+    layers 0-10 (>= 32 packed tokens, >= 16 for one sequence), bit for bit."""
+    seqs, layers = {"ragged_l1": (ragged_batch(3, 5, 70, 17), 1), "ragged_l11": (ragged_batch(4, 3, 90, 19), 11),
+                    "single16": (ragged_batch(1, 20, 20, 3), 2), "single_short": (ragged_batch(1, 12, 12, 3), 2),
+                    "fused_ffn": (ragged_batch(10, 400, 512, 29), 1)}[case]
+    h, q, sc = engine.forward_prefix(ws_quant, seqs, layers)
+    rh, rq, rsc = oracle_model.run_prefix_sme(seqs, layers)
+    assert np.array_equal(h, rh) and np.array_equal(q, rq) and np.array_equal(sc, rsc)
+    if case == "ragged_l1":  # the mode changed the state: the exact path differs
+        eh, _, _ = oracle_model.run_prefix(seqs, layers)
+        assert not np.array_equal(h, eh)
