@@ -176,6 +176,7 @@ def main():
     ap.add_argument("--cpu-sample", type=int, default=256, help="sequences of the workload timed on the CPU")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-c1", action="store_true", help="skip the 128-token latency measurement")
+    ap.add_argument("--no-quantized", action="store_true", help="skip the quantized-attention mode pass")
     ap.add_argument("--gemm", action="store_true", help="run only the configs[1] GEMM microbench")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one plain device copy of this many MiB first (calibrates rocprofv3 byte counters)")
@@ -275,6 +276,36 @@ def main():
         s = ktimes[k][0] / 1e3 / max(1, ktimes[k][1])
         ffn[k] = round(a / s / 1e12 / p, 4)
 
+    # the reference's ArmSme attention (int8 Q/K/V, int16 P; AE_ATTENTION_QUANTIZED) on the same batch:
+    # an optional mode, reported beside the exact path's figures, never as `value`
+    quant = None
+    if not args.no_quantized:
+        ws.set_attention_mode(True)
+        for _ in range(max(2, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        q0, q1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        q0.record(stream)
+        for _ in range(args.steps):
+            step()
+        q1.record(stream)
+        torch.cuda.synchronize()
+        q_ms = q0.elapsed_time(q1)
+        emb_q = out_d.cpu().numpy().astype(np.float64)
+        ws.set_timing(True)
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        kq = ws.kernel_times()
+        ws.set_timing(False)
+        ws.set_attention_mode(False)
+        e64 = emb.astype(np.float64)
+        cos_q = float(((e64 * emb_q).sum(1) / (np.linalg.norm(e64, axis=1) * np.linalg.norm(emb_q, axis=1))).min())
+        quant = {"value": round(B * args.steps / (q_ms / 1e3), 2), "unit": "embeddings/s",
+                 "ms_per_step": round(q_ms / args.steps, 4),
+                 "attention_ms_per_step": round(kq["attention"][0] / max(1, args.steps), 4),
+                 "min_cos_vs_exact": round(cos_q, 6)}
+
     # ms/seq @ 128 tokens (BASELINE metric, part 3): single-sequence latency, device-resident input
     c1_ms = None
     if not args.no_c1:
@@ -358,7 +389,7 @@ def main():
         "wall_s": round(wall, 4), "outputs_unit_norm": norms_ok,
         "ffn_int8_mfma_frac": ffn, "ms_per_seq_128": c1_ms,
         "kernel_ms_per_step": {k: round(v, 4) for k, v in kernel_ms.items()},
-        "roofline": roofline, "e2e_roofline": e2e, "cpu_baseline": cpu,
+        "roofline": roofline, "e2e_roofline": e2e, "cpu_baseline": cpu, "quantized_attention_mode": quant,
     }
     print(json.dumps(line), flush=True)
     ws.close()

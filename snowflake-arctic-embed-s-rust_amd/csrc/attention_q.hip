@@ -96,11 +96,46 @@ __global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, 
       s.ks[t * 12 + h] = quant_row32(row + H, k_mul, s.k8 + (size_t)t * H + h * 32);
     }
   }
-  for (int c = tid; c < H; c += 256) {
-    float m = 0.0f;
-    const int n = min(64, T - t0);
-    for (int i = 0; i < n; i++) m = vmax(m, fabsf(qkv[(size_t)(t0 + i) * HQKV + 2 * H + c]));
-    atomicMax(&s.vmax[c], __float_as_uint(m));
+  __shared__ float s_m[4][H];
+  {  // wave w: tokens t0 + w + 4i; lane: columns lane + 64k (row-contiguous loads)
+    const int w = tid >> 6, lane = tid & 63, n = min(64, T - t0);
+    float m[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = w; i < n; i += 4) {
+      const float* vr = qkv + (size_t)(t0 + i) * HQKV + 2 * H + lane;
+#pragma unroll
+      for (int k = 0; k < 6; k++) m[k] = vmax(m[k], fabsf(vr[64 * k]));
+    }
+#pragma unroll
+    for (int k = 0; k < 6; k++) s_m[w][lane + 64 * k] = m[k];
+  }
+  __syncthreads();
+  for (int c = tid; c < H; c += 256)
+    atomicMax(&s.vmax[c], __float_as_uint(vmax(vmax(s_m[0][c], s_m[1][c]), vmax(s_m[2][c], s_m[3][c]))));
+}
+
+// V to int8 with the batch's per-column scales (quantize_v_row_neon), stored
+// transposed: s.vt[c][round8(cu[b] + 7b) + (t - cu[b])] for token t of segment b.
+// Workgroup (64-token block, head): the block's V columns are staged in LDS so
+// that both the f32 reads and the int8 writes are row-contiguous.
+__global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const int* cu, int B, int T, SmeArgs s,
+                                                         size_t vt_len) {
+  __shared__ float sv[64][33];
+  __shared__ float s_inv[32];
+  __shared__ size_t s_pos[64];
+  const int tid = threadIdx.x, t0 = blockIdx.x * 64, h = blockIdx.y;
+  if (tid < 32) s_inv[tid] = 127.0f / __uint_as_float(s.vmax[h * 32 + tid]);
+  if (tid >= 64 && tid < 128 && t0 + tid - 64 < T) {
+    const int t = t0 + tid - 64, b = find_segment(cu, B, t);
+    s_pos[tid - 64] = (size_t)((cu[b] + 7 * b + 7) & ~7) + (size_t)(t - cu[b]);
+  }
+  for (int i = tid; i < 64 * 32; i += 256) {
+    const int r = i >> 5, c = i & 31;
+    sv[r][c] = t0 + r < T ? qkv[(size_t)(t0 + r) * HQKV + 2 * H + h * 32 + c] : 0.0f;
+  }
+  __syncthreads();
+  for (int i = tid; i < 64 * 32; i += 256) {
+    const int c = i >> 6, r = i & 63, t = t0 + r;
+    if (t < T) s.vt[(size_t)(h * 32 + c) * vt_len + s_pos[r]] = (int8_t)sat8(cvtn(sv[r][c] * s_inv[c]));
   }
 }
 
@@ -108,10 +143,10 @@ __global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, 
 // kernel's tile records and XCD-contiguous numbering.  S[32][pitch] holds the
 // scores, then (in place, each element by the thread that read it) the int32
 // quantized probabilities.
-__global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles) {
+__global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles, size_t vt_len) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kSmeQ];
-  __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32], s_vinv[32];
+  __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32];
   const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
   const int h = item / max_tiles, tile = item - h * max_tiles;
   const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
@@ -128,7 +163,6 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   if (tid < 32) {
     const float vm = __uint_as_float(sa.vmax[h * 32 + tid]);
     s_vscale[tid] = vm * (1.0f / 127.0f);
-    s_vinv[tid] = 127.0f / vm;
   }
 
   // phase 1: integer scores, A = Q (16 queries x 32 dims), B = K (32 dims x 16
@@ -188,7 +222,19 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
     const float* srow = S + row * pitch;
     int isum = 0;
     const bool live = row < nq;  // rows past the tile's queries hold no scores
-    for (int j = sub; j < nv; j += 8) {
+    int j = sub;
+    for (; j + 24 < nv; j += 32) {  // four keys per lane in flight
+      float x[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) x[u] = srow[j + 8 * u];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int q = exp2_q16(live ? x[u] - m : -16.0f);
+        prow[j + 8 * u] = q;
+        isum += q;
+      }
+    }
+    for (; j < nv; j += 8) {
       const int q = exp2_q16(live ? srow[j] - m : -16.0f);
       prow[j] = q;
       isum += q;
@@ -213,46 +259,50 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
 
   // phase 3: ctx = P @ V over chunks of 32 keys.  Wave w owns the 16 x 16
   // (query, dim) quadrant (w / 2, w % 2).  p < 2^14 is split as 128 p_hi + p_lo
-  // (both in [0, 127]) so the int8 MFMA takes it; V is quantized on load.  The
-  // integer sums are exact, so ctx = f32(128 acc_hi + acc_lo) * (v_scale * p_scale).
+  // (both in [0, 127]) so the int8 MFMA takes it.  The integer sums are exact,
+  // so ctx = f32(128 acc_hi + acc_lo) * (v_scale * p_scale).
   const int qh = wave >> 1, dh = wave & 1;
   if (qh < nqh) {
     const int c = 16 * dh + lr;
-    const float vinv = s_vinv[c];
     const int* prow = Si + (16 * qh + lr) * pitch;
-    const float* vcol = p.qkv + (size_t)s0 * HQKV + 2 * H + h * 32 + c;
+    // this lane's int8 V for every chunk: keys t0 + 8(l/16) .. +7 of column c, one
+    // aligned 8-byte load each (keys past the segment meet p = 0)
+    const int b = find_segment(p.cu, p.B, s0);
+    const int8_t* vrow = sa.vt + (size_t)(h * 32 + c) * vt_len + ((p.cu[b] + 7 * b + 7) & ~7) + 8 * lg;
+    const int nch = (L + 31) >> 5;
+    v_i64 vb[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (k < nch) vb[k] = *reinterpret_cast<const v_i64*>(vrow + 32 * k);
     v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
-    for (int t0 = 0; t0 < L; t0 += 32) {  // wave-uniform
-      const int tb8 = t0 + 8 * lg;  // this lane's 8 keys
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      if (k >= nch) break;  // wave-uniform
+      const int tb8 = 32 * k + 8 * lg;  // this lane's 8 keys
       int pv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       if (tb8 < L) {  // reads stay below round8(L) <= pitch - 4
-        const int4 a = reinterpret_cast<const int4*>(prow + tb8)[0];
-        const int4 b = reinterpret_cast<const int4*>(prow + tb8)[1];
-        pv[0] = a.x; pv[1] = a.y; pv[2] = a.z; pv[3] = a.w;
-        pv[4] = b.x; pv[5] = b.y; pv[6] = b.z; pv[7] = b.w;
+        const int4 x = reinterpret_cast<const int4*>(prow + tb8)[0];
+        const int4 y = reinterpret_cast<const int4*>(prow + tb8)[1];
+        pv[0] = x.x; pv[1] = x.y; pv[2] = x.z; pv[3] = x.w;
+        pv[4] = y.x; pv[5] = y.y; pv[6] = y.z; pv[7] = y.w;
       }
-      uint32_t hi[2], lo[2], vb[2];
+      uint32_t hi[2], lo[2];
 #pragma unroll
       for (int w2 = 0; w2 < 2; w2++) {
-        int ph[4], pl[4], vq[4];
+        int ph[4], pl[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int k = 4 * w2 + i, t = tb8 + k;
-          const int pk = t < L ? pv[k] : 0;
+          const int pk = tb8 + 4 * w2 + i < L ? pv[4 * w2 + i] : 0;
           ph[i] = pk >> 7;
           pl[i] = pk & 127;
-          const float v = vcol[(size_t)min(t, L - 1) * HQKV];
-          vq[i] = t < L ? sat8(cvtn(v * vinv)) : 0;
         }
         hi[w2] = pack4(ph[0], ph[1], ph[2], ph[3]);
         lo[w2] = pack4(pl[0], pl[1], pl[2], pl[3]);
-        vb[w2] = pack4(vq[0], vq[1], vq[2], vq[3]);
       }
       const v_i64 ah = (v_i64)(((uint64_t)hi[1] << 32) | hi[0]);
       const v_i64 al = (v_i64)(((uint64_t)lo[1] << 32) | lo[0]);
-      const v_i64 bv = (v_i64)(((uint64_t)vb[1] << 32) | vb[0]);
-      acc_hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, bv, acc_hi, 0, 0, 0);
-      acc_lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, bv, acc_lo, 0, 0, 0);
+      acc_hi = __builtin_amdgcn_mfma_i32_16x16x32_i8(ah, vb[k], acc_hi, 0, 0, 0);
+      acc_lo = __builtin_amdgcn_mfma_i32_16x16x32_i8(al, vb[k], acc_lo, 0, 0, 0);
     }
     const int qb = 16 * qh + 4 * lg;
     const float vsc = s_vscale[c];
@@ -278,10 +328,12 @@ void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_
   if (T <= 0 || p.B <= 0) return;
   launch_fill_u32(s.vmax, H, 0x322bcc77u, st);  // bits of 1e-8f
   hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(256), 0, st, p.qkv, T, s);
+  const size_t vt_len = sme_vt_len(T, p.B);
+  hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
   if (plan) launch_attention_plan(p, T, st);
   const int max_tiles = attention_max_tiles(p.B, T);
   hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p, s,
-                     max_tiles);
+                     max_tiles, vt_len);
 }
 
 void init_attention_sme_kernels() {

@@ -915,8 +915,8 @@ static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev,
                   aek::attention_pitch(std::min(max_len, ae::kMaxPos))};
   void* sme = nullptr;
   if (quantized) {  // int8 Q, K [T,384] each, their scales [T,12] each, the |V| column max [384]
-    const size_t T = size_t(total_tokens);
-    hipError_t e = hipMalloc(&sme, T * 384 * 2 + T * 12 * 4 * 2 + 384 * 4);
+    const size_t T = size_t(total_tokens), vt = aek::sme_vt_len(total_tokens, n_seqs);
+    hipError_t e = hipMalloc(&sme, T * 384 * 2 + T * 12 * 4 * 2 + 384 * 4 + 384 * vt);
     if (e != hipSuccess) {
       (void)hipFree(plan);
       return fail(AE_ERR_HIP, std::string("attention scratch: ") + hipGetErrorString(e));
@@ -924,7 +924,8 @@ static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev,
     char* b = static_cast<char*>(sme);
     aek::SmeArgs sa{reinterpret_cast<int8_t*>(b), reinterpret_cast<int8_t*>(b + T * 384),
                     reinterpret_cast<float*>(b + T * 768), reinterpret_cast<float*>(b + T * 768 + T * 48),
-                    reinterpret_cast<uint32_t*>(b + T * 768 + T * 96)};
+                    reinterpret_cast<uint32_t*>(b + T * 768 + T * 96),
+                    reinterpret_cast<int8_t*>(b + T * 768 + T * 96 + 384 * 4)};
     aek::init_attention_sme_kernels();
     aek::launch_attention_sme(a, sa, total_tokens, as_stream(stream));
   } else {
@@ -982,13 +983,15 @@ int ae_workspace_set_attention_mode(ae_workspace* ws, int mode) {
     const size_t T = size_t(ws->max_tokens);
     int rc;
     if ((rc = dalloc(&ws->sme.q8, T * 384)) || (rc = dalloc(&ws->sme.k8, T * 384)) || (rc = dalloc(&ws->sme.qs, T * 12)) ||
-        (rc = dalloc(&ws->sme.ks, T * 12)) || (rc = dalloc(&ws->sme.vmax, size_t(384))))
+        (rc = dalloc(&ws->sme.ks, T * 12)) || (rc = dalloc(&ws->sme.vmax, size_t(384))) ||
+        (rc = dalloc(&ws->sme.vt, 384 * aek::sme_vt_len(ws->max_tokens, ws->max_seqs))))
       return rc;
     ws->dev.push_back(ws->sme.q8);
     ws->dev.push_back(ws->sme.k8);
     ws->dev.push_back(ws->sme.qs);
     ws->dev.push_back(ws->sme.ks);
     ws->dev.push_back(ws->sme.vmax);
+    ws->dev.push_back(ws->sme.vt);
     aek::init_attention_sme_kernels();
   }
   ws->attention_mode = mode;

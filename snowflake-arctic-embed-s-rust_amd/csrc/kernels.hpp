@@ -122,7 +122,10 @@ struct SmeArgs {
   float* qs;        // [T,12]
   float* ks;        // [T,12]
   uint32_t* vmax;   // [384], f32 bits
+  int8_t* vt;       // [384][sme_vt_len(T, B)]: int8 V per head column, keys contiguous; segment b
+                    // starts at round8(cu[b] + 7b), so every 8-key group is 8-byte aligned
 };
+inline size_t sme_vt_len(int T, int B) { return ((size_t)T + 7 * (size_t)B + 64 + 7) & ~(size_t)7; }
 // the packing, the plan (plan = true) and the attention; p.smooth / p.rowmax as launch_attention
 void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan = true);
 void init_attention_sme_kernels();  // once per device before the first launch
