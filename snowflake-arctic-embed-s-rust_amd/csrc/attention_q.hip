@@ -165,6 +165,21 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
     s_vscale[tid] = vm * (1.0f / 127.0f);
   }
 
+  // this lane's int8 V for phase 3, issued first so that its latency hides
+  // behind phases 1 and 2: keys 32k + 8(l/16) .. +7 of column c = 16(w % 2) +
+  // l % 16, one aligned 8-byte load per 32-key chunk k (keys past the segment
+  // meet p = 0)
+  const int nch = (L + 31) >> 5;
+  v_i64 vb[16];
+  {
+    const int b = find_segment(p.cu, p.B, s0);
+    const int8_t* vrow =
+        sa.vt + (size_t)(h * 32 + 16 * (wave & 1) + lr) * vt_len + ((p.cu[b] + 7 * b + 7) & ~7) + 8 * lg;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+      if (k < nch) vb[k] = *reinterpret_cast<const v_i64*>(vrow + 32 * k);
+  }
+
   // phase 1: integer scores, A = Q (16 queries x 32 dims), B = K (32 dims x 16
   // keys), one v_mfma_i32_16x16x32_i8 per (key block, query half); lane l
   // supplies row l % 16 and dims 8(l/16)..+7 of both, and ends with queries
@@ -185,10 +200,23 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   for (int qh = 0; qh < 2; qh++)
 #pragma unroll
     for (int r = 0; r < 4; r++) mrow[qh][r] = -INFINITY;
-  for (int kb = wave; kb < nkb; kb += 4) {  // wave-uniform
-    const int key = min(16 * kb + lr, L - 1);
-    const v_i64 kv = *reinterpret_cast<const v_i64*>(sa.k8 + (size_t)(s0 + key) * H + h * 32 + 8 * lg);
-    const float ksc = sa.ks[(s0 + key) * 12 + h];
+  // all of this wave's K blocks (kb = wave + 4i, at most 8) are loaded up front
+  v_i64 kvs[8];
+  float kss[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int key = min(16 * (wave + 4 * i) + lr, L - 1);
+    if (wave + 4 * i < nkb) {
+      kvs[i] = *reinterpret_cast<const v_i64*>(sa.k8 + (size_t)(s0 + key) * H + h * 32 + 8 * lg);
+      kss[i] = sa.ks[(s0 + key) * 12 + h];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int kb = wave + 4 * i;
+    if (kb >= nkb) break;  // wave-uniform
+    const v_i64 kv = kvs[i];
+    const float ksc = kss[i];
 #pragma unroll
     for (int qh = 0; qh < 2; qh++) {
       if (qh >= nqh) break;  // wave-uniform
@@ -265,15 +293,6 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   if (qh < nqh) {
     const int c = 16 * dh + lr;
     const int* prow = Si + (16 * qh + lr) * pitch;
-    // this lane's int8 V for every chunk: keys t0 + 8(l/16) .. +7 of column c, one
-    // aligned 8-byte load each (keys past the segment meet p = 0)
-    const int b = find_segment(p.cu, p.B, s0);
-    const int8_t* vrow = sa.vt + (size_t)(h * 32 + c) * vt_len + ((p.cu[b] + 7 * b + 7) & ~7) + 8 * lg;
-    const int nch = (L + 31) >> 5;
-    v_i64 vb[16];
-#pragma unroll
-    for (int k = 0; k < 16; k++)
-      if (k < nch) vb[k] = *reinterpret_cast<const v_i64*>(vrow + 32 * k);
     v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < 16; k++) {
