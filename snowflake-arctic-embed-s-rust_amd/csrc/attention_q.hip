@@ -22,6 +22,10 @@ namespace aek {
 
 namespace {
 constexpr int kSmeQ = 32;  // queries per workgroup (the exact kernel's tile plan)
+// int16 P tile: row pitch round16(max length) + 8 (s_pitch = round16 + 4), a
+// multiple of 8 so that every 8-key group is one aligned 16-byte LDS read
+__host__ __device__ inline int sme_p_pitch(int s_pitch) { return s_pitch + 4; }
+inline size_t sme_p_bytes(int s_pitch) { return (size_t)kSmeQ * sme_p_pitch(s_pitch) * 2; }
 typedef long v_i64;
 
 // vcvtnq_s32_f32 on in-range values: round to nearest, ties to even
@@ -140,22 +144,21 @@ __global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const
 }
 
 // One workgroup per (head, tile of 32 queries of one segment), the exact
-// kernel's tile records and XCD-contiguous numbering.  S[32][pitch] holds the
-// scores, then (in place, each element by the thread that read it) the int32
-// quantized probabilities.
+// kernel's tile records and XCD-contiguous numbering.  The only LDS tile is the
+// int16 P[32][pitch16] (33 KB at 512 keys): several workgroups per CU.
 __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles, size_t vt_len) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kSmeQ];
   __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32];
+  __shared__ int s_isum[kSmeQ];
   const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
   const int h = item / max_tiles, tile = item - h * max_tiles;
   const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
   const int nq = rec.w;
   if (nq == 0) return;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;
-  const int pitch = p.s_pitch;
-  float* S = smem;
-  int* Si = reinterpret_cast<int*>(smem);
+  const int pitch16 = sme_p_pitch(p.s_pitch);
+  int16_t* P = reinterpret_cast<int16_t*>(smem);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
@@ -163,6 +166,7 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   if (tid < 32) {
     const float vm = __uint_as_float(sa.vmax[h * 32 + tid]);
     s_vscale[tid] = vm * (1.0f / 127.0f);
+    s_isum[tid] = 0;
   }
 
   // this lane's int8 V for phase 3, issued first so that its latency hides
@@ -224,7 +228,6 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const float sc = ((float)acc[r] * ksc) * qsc[qh][r];
-        S[(16 * qh + 4 * lg + r) * pitch + 16 * kb + lr] = sc;  // 16kb + lr < round16(L) <= pitch - 4
         mrow[qh][r] = vmax(mrow[qh][r], sc);
       }
     }
@@ -240,49 +243,49 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   if (tid < kSmeQ) s_max[tid] = fmaxf(fmaxf(s_maxw[0][tid], s_maxw[1][tid]), fmaxf(s_maxw[2][tid], s_maxw[3][tid]));
   __syncthreads();
 
-  // phase 2: p = round(16383 * 2^(s - max)) in place, 8 lanes per row (row
-  // tid / 8): the cubic over the first nv = L & ~7 keys, glibc exp2f over the
-  // last L - nv; the integer row sum is order-free.
+  // phase 2: the same scores again (the int8 MFMAs are cheap; recomputing
+  // them is bit-identical and keeps the tile small), p = round(16383 *
+  // 2^(s - max)) into the int16 tile P[32][pitch16]: the cubic for keys below
+  // nv = L & ~7, glibc exp2f (half-away rounding) for the last L - nv, 0 for the
+  // padding keys of the last block.  The integer row sums are order-free.
   {
-    const int row = tid >> 3, sub = tid & 7, nv = L & ~7;
-    const float m = s_max[row];
-    int* prow = Si + row * pitch;
-    const float* srow = S + row * pitch;
-    int isum = 0;
-    const bool live = row < nq;  // rows past the tile's queries hold no scores
-    int j = sub;
-    for (; j + 24 < nv; j += 32) {  // four keys per lane in flight
-      float x[4];
+    const int nv = L & ~7;
+    float mq[2][4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) x[u] = srow[j + 8 * u];
+    for (int qh = 0; qh < 2; qh++)
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const int q = exp2_q16(live ? x[u] - m : -16.0f);
-        prow[j + 8 * u] = q;
-        isum += q;
+      for (int r = 0; r < 4; r++) mq[qh][r] = s_max[16 * qh + 4 * lg + r];
+    int isum[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int kb = wave + 4 * i;
+      if (kb >= nkb) break;  // wave-uniform
+      const int key = 16 * kb + lr;
+      const bool tail_blk = 16 * kb + 15 >= nv;  // wave-uniform: the block reaches the exp2f keys
+#pragma unroll
+      for (int qh = 0; qh < 2; qh++) {
+        if (qh >= nqh) break;  // wave-uniform
+        const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[qh], kvs[i], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float x = ((float)acc[r] * kss[i]) * qsc[qh][r] - mq[qh][r];
+          int q = exp2_q16(key < nv ? x : -16.0f);
+          if (tail_blk) {
+            const float e = exp2f_libm(key >= nv && key < L ? x : 0.0f, tb);
+            if (key >= nv) q = key < L ? min(16383, max(0, cvtn_away(e * 16383.0f))) : 0;
+          }
+          P[(16 * qh + 4 * lg + r) * pitch16 + key] = (int16_t)q;  // key < round16(L) <= pitch16 - 8
+          isum[qh][r] += q;
+        }
       }
     }
-    for (; j < nv; j += 8) {
-      const int q = exp2_q16(live ? srow[j] - m : -16.0f);
-      prow[j] = q;
-      isum += q;
-    }
-    {  // every lane evaluates (exp2f_libm needs the whole wave); lanes past L discard
-      const int j = nv + sub;
-      const bool in = live && j < L;
-      const float e = exp2f_libm(in ? srow[j] - m : 0.0f, tb);
-      int q = cvtn_away(e * 16383.0f);
-      q = min(16383, max(0, q));
-      if (in) {
-        prow[j] = q;
-        isum += q;
-      }
-    }
-    isum += __shfl_xor(isum, 1, 64);
-    isum += __shfl_xor(isum, 2, 64);
-    isum += __shfl_xor(isum, 4, 64);
-    if (sub == 0) s_pscale[row] = 1.0f / (float)max(isum, 1);
+#pragma unroll
+    for (int qh = 0; qh < 2; qh++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) atomicAdd(&s_isum[16 * qh + 4 * lg + r], isum[qh][r]);
   }
+  __syncthreads();
+  if (tid < kSmeQ) s_pscale[tid] = 1.0f / (float)max(s_isum[tid], 1);
   __syncthreads();
 
   // phase 3: ctx = P @ V over chunks of 32 keys.  Wave w owns the 16 x 16
@@ -292,18 +295,21 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   const int qh = wave >> 1, dh = wave & 1;
   if (qh < nqh) {
     const int c = 16 * dh + lr;
-    const int* prow = Si + (16 * qh + lr) * pitch;
+    const int16_t* prow = P + (16 * qh + lr) * pitch16;
     v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       if (k >= nch) break;  // wave-uniform
       const int tb8 = 32 * k + 8 * lg;  // this lane's 8 keys
       int pv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (tb8 < L) {  // reads stay below round8(L) <= pitch - 4
-        const int4 x = reinterpret_cast<const int4*>(prow + tb8)[0];
-        const int4 y = reinterpret_cast<const int4*>(prow + tb8)[1];
-        pv[0] = x.x; pv[1] = x.y; pv[2] = x.z; pv[3] = x.w;
-        pv[4] = y.x; pv[5] = y.y; pv[6] = y.z; pv[7] = y.w;
+      if (tb8 < L) {  // reads stay below round8(L) <= pitch16 - 8
+        const int4 x = *reinterpret_cast<const int4*>(prow + tb8);
+        const int w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          pv[2 * i] = w4[i] & 0xffff;  // p >= 0: the low half is the key's value
+          pv[2 * i + 1] = (int)((uint32_t)w4[i] >> 16);
+        }
       }
       uint32_t hi[2], lo[2];
 #pragma unroll
@@ -351,13 +357,13 @@ void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_
   hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
   if (plan) launch_attention_plan(p, T, st);
   const int max_tiles = attention_max_tiles(p.B, T);
-  hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), attention_lds_bytes(p.s_pitch), st, p, s,
+  hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), sme_p_bytes(p.s_pitch), st, p, s,
                      max_tiles, vt_len);
 }
 
 void init_attention_sme_kernels() {
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(sme_attention_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)attention_lds_bytes(attention_pitch(512)));
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)sme_p_bytes(attention_pitch(512)));
 }
 
 }  // namespace aek
