@@ -261,7 +261,6 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
       const int kb = wave + 4 * i;
       if (kb >= nkb) break;  // wave-uniform
       const int key = 16 * kb + lr;
-      const bool tail_blk = 16 * kb + 15 >= nv;  // wave-uniform: the block reaches the exp2f keys
 #pragma unroll
       for (int qh = 0; qh < 2; qh++) {
         if (qh >= nqh) break;  // wave-uniform
@@ -269,13 +268,33 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float x = ((float)acc[r] * kss[i]) * qsc[qh][r] - mq[qh][r];
-          int q = exp2_q16(key < nv ? x : -16.0f);
-          if (tail_blk) {
-            const float e = exp2f_libm(key >= nv && key < L ? x : 0.0f, tb);
-            if (key >= nv) q = key < L ? min(16383, max(0, cvtn_away(e * 16383.0f))) : 0;
-          }
+          const int q = exp2_q16(key < nv ? x : -16.0f);  // keys from nv on: 0 here, set below
           P[(16 * qh + 4 * lg + r) * pitch16 + key] = (int16_t)q;  // key < round16(L) <= pitch16 - 8
           isum[qh][r] += q;
+        }
+      }
+    }
+    // the last L - nv (< 8) keys lie in block nv / 16: its wave overwrites their
+    // zeros with the exp2f values (the scores computed once more, bit-identical)
+    if (nv < L && wave == ((nv >> 4) & 3)) {  // wave-uniform
+      const int key = (nv & ~15) + lr;
+      const int krow = s0 + min(key, L - 1);
+      const v_i64 kv = *reinterpret_cast<const v_i64*>(sa.k8 + (size_t)krow * H + h * 32 + 8 * lg);
+      const float ksc = sa.ks[krow * 12 + h];
+      const bool in = key >= nv && key < L;
+#pragma unroll
+      for (int qh = 0; qh < 2; qh++) {
+        if (qh >= nqh) break;  // wave-uniform
+        const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[qh], kv, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float x = ((float)acc[r] * ksc) * qsc[qh][r] - mq[qh][r];
+          const float e = exp2f_libm(in ? x : 0.0f, tb);  // every lane evaluates (the table lookup)
+          if (in) {
+            const int q = min(16383, max(0, cvtn_away(e * 16383.0f)));
+            P[(16 * qh + 4 * lg + r) * pitch16 + key] = (int16_t)q;
+            isum[qh][r] += q;
+          }
         }
       }
     }
