@@ -88,11 +88,11 @@ __device__ __forceinline__ int exp2_q16(float x) {
 // Q and K of every token and head to int8 with their scales, and the per-column
 // |V| maximum over the batch folded into s.vmax (atomicMax on f32 bits; the
 // buffer is preset to bits(1e-8f), the reference's starting value).
-// 64 tokens per workgroup.
-__global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, SmeArgs s) {
+// 64 tokens per workgroup of 12 waves.
+__global__ __launch_bounds__(768) void sme_pack_kernel(const float* qkv, int T, SmeArgs s) {
   const int tid = threadIdx.x, t0 = blockIdx.x * 64;
   const float k_mul = kInvSqrtD * 1.44269504088896340736f;  // inv_sqrt_d * LOG2_E in f32
-  for (int it = tid; it < 64 * 12; it += 256) {
+  for (int it = tid; it < 64 * 12; it += 768) {  // one (token, head) per thread
     const int t = t0 + it / 12, h = it % 12;
     if (t < T) {
       const float* row = qkv + (size_t)t * HQKV + h * 32;
@@ -100,11 +100,11 @@ __global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, 
       s.ks[t * 12 + h] = quant_row32(row + H, k_mul, s.k8 + (size_t)t * H + h * 32);
     }
   }
-  __shared__ float s_m[4][H];
-  {  // wave w: tokens t0 + w + 4i; lane: columns lane + 64k (row-contiguous loads)
+  __shared__ float s_m[12][H];
+  {  // wave w: tokens t0 + w + 12i; lane: columns lane + 64k (row-contiguous loads)
     const int w = tid >> 6, lane = tid & 63, n = min(64, T - t0);
     float m[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = w; i < n; i += 4) {
+    for (int i = w; i < n; i += 12) {
       const float* vr = qkv + (size_t)(t0 + i) * HQKV + 2 * H + lane;
 #pragma unroll
       for (int k = 0; k < 6; k++) m[k] = vmax(m[k], fabsf(vr[64 * k]));
@@ -113,8 +113,12 @@ __global__ __launch_bounds__(256) void sme_pack_kernel(const float* qkv, int T, 
     for (int k = 0; k < 6; k++) s_m[w][lane + 64 * k] = m[k];
   }
   __syncthreads();
-  for (int c = tid; c < H; c += 256)
-    atomicMax(&s.vmax[c], __float_as_uint(vmax(vmax(s_m[0][c], s_m[1][c]), vmax(s_m[2][c], s_m[3][c]))));
+  for (int c = tid; c < H; c += 768) {
+    float m = s_m[0][c];
+#pragma unroll
+    for (int w = 1; w < 12; w++) m = vmax(m, s_m[w][c]);
+    atomicMax(&s.vmax[c], __float_as_uint(m));
+  }
 }
 
 // V to int8 with the batch's per-column scales (quantize_v_row_neon), stored
@@ -371,7 +375,7 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
 void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan) {
   if (T <= 0 || p.B <= 0) return;
   launch_fill_u32(s.vmax, H, 0x322bcc77u, st);  // bits of 1e-8f
-  hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(256), 0, st, p.qkv, T, s);
+  hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(768), 0, st, p.qkv, T, s);
   const size_t vt_len = sme_vt_len(T, p.B);
   hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
   if (plan) launch_attention_plan(p, T, st);
