@@ -102,16 +102,23 @@ def roofline_step_ms(T, B, lens, ffn_fused=False):
 
 
 def host_cpu():
-    """The host's CPU model and the ISA extensions the reference's x86 dispatch looks at."""
-    model, flags = "unknown", set()
+    """The host's CPU: /proc/cpuinfo's model name with its family / model / stepping numbers
+    (some hosts report only a generic name), and the ISA extensions the reference's x86 dispatch
+    looks at."""
+    info, flags = {}, set()
     try:
         for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name") and model == "unknown":
-                model = ln.split(":", 1)[1].strip()
-            elif ln.startswith("flags") and not flags:
-                flags = set(ln.split(":", 1)[1].split())
+            k, _, v = ln.partition(":")
+            k = k.strip()
+            if k in ("model name", "vendor_id", "cpu family", "model", "stepping") and k not in info:
+                info[k] = v.strip()
+            elif k == "flags" and not flags:
+                flags = set(v.split())
     except OSError:
         pass
+    model = "%s (%s family %s model %s stepping %s)" % (info.get("model name", "unknown"), info.get("vendor_id", "?"),
+                                                         info.get("cpu family", "?"), info.get("model", "?"),
+                                                         info.get("stepping", "?"))
     return model, [f for f in ("avx2", "fma", "avx_vnni", "avx512f", "avx512_vnni") if f in flags]
 
 
@@ -333,7 +340,10 @@ def main():
     cpu = None
     if not args.no_cpu:
         orc = load_cpu_oracle()
-        threads = max(1, min(16, os.cpu_count() or 1))
+        # all the host cores this process may use (the reference's bin uses available_parallelism,
+        # src/bin/arctic_embed.rs:324-326), capped at the 16 CPUs a one-GPU job gets on the GPU box
+        usable = len(os.sched_getaffinity(0))
+        threads = max(1, min(16, usable))
         sample = seqs[: args.cpu_sample]
         m = None
         tmp = tempfile.mkdtemp(prefix="ae_cpu_")
@@ -343,40 +353,44 @@ def main():
         finally:
             shutil.rmtree(tmp, ignore_errors=True)
         # the reference's best x86 backend (AVX-VNNI, else AVX2; restated in oracle/x86.c) under its
-        # embed_batch policy with all threads: warm-up on the first 32 items, median of 3 full runs;
-        # the scalar restatement only on a host without AVX2+FMA
+        # embed_batch policy: warm-up on the first 32 items (src/bin/arctic_embed.rs:338), then the
+        # median of 5 full runs; the scalar restatement only on a host without AVX2+FMA
         backend = orc.x86_backend()
-        run = (lambda s: m.x86_embed_batch_tokens(s, threads)) if backend else \
-              (lambda s: m.embed_batch_tokens(s, threads))
-        run(sample[:32])
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            ref = run(sample)
-            times.append(time.perf_counter() - t0)
-        cpu_s = sorted(times)[1]
-        # ms/seq at 128 tokens on one thread (configs[0]'s sequence; median of 5)
+
+        def run(s, n_threads):
+            return m.x86_embed_batch_tokens(s, n_threads) if backend else m.embed_batch_tokens(s, n_threads)
+
+        def median_s(fn, reps):
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return sorted(ts)[reps // 2]
+
+        run(sample[:32], threads)
+        ref = run(sample, threads)
+        cpu_s = median_s(lambda: run(sample, threads), 5)
+        # ms/seq at 128 tokens (configs[0]'s sequence): one thread, and all threads (the reference's
+        # embed_batch gives one sequence to one thread, so more threads cannot shorten it); median of 5
         c1seq = make_batch(1, 128, 128, 1)
-        one = (lambda s: m.x86_embed_batch_tokens(s, 1)) if backend else (lambda s: m.embed_batch_tokens(s, 1))
-        one(c1seq)
-        t1 = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            one(c1seq)
-            t1.append(time.perf_counter() - t0)
-        cpu_c1_ms = sorted(t1)[2] * 1e3
+        run(c1seq, 1)
+        cpu_c1_ms = median_s(lambda: run(c1seq, 1), 5) * 1e3
+        cpu_c1_all_ms = median_s(lambda: run(c1seq, threads), 5) * 1e3
         m.close()
         g = emb[: len(sample)].astype(np.float64)
         r = np.asarray(ref, np.float64)
         cos = float(((g * r).sum(1) / (np.linalg.norm(g, axis=1) * np.linalg.norm(r, axis=1))).min())
         cpu_model, isa = host_cpu()
         cpu = {"value": round(len(sample) / cpu_s, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
-               "backend": backend or "scalar",
+               "backend": backend or "scalar", "os_cpu_count": os.cpu_count(), "usable_cpus": usable,
                "tokens_per_s": round(sum(len(s) for s in sample) / cpu_s, 1),
-               "ms_per_seq_128_1thread": round(cpu_c1_ms, 3), "cpu_model": cpu_model, "isa": isa,
-               "sample": "first %d sequences (%d tokens) of the %s batch, median of 3 runs; restatement of the "
-                         "reference's %s backend under its embed_batch policy"
-                         % (len(sample), sum(len(s) for s in sample), workload,
+               "ms_per_seq_128_1thread": round(cpu_c1_ms, 3), "ms_per_seq_128_all_threads": round(cpu_c1_all_ms, 3),
+               "cpu_model": cpu_model, "isa": isa,
+               "sample": "first %d sequences (%d tokens) of the %s batch, median of 5 runs on %d threads (all usable "
+                         "CPUs, at most the GPU box's 16 per GPU); restatement of the reference's %s backend under "
+                         "its embed_batch policy"
+                         % (len(sample), sum(len(s) for s in sample), workload, threads,
                             {"avx_vnni": "AVX-VNNI", "avx2": "AVX2"}.get(backend, "scalar")),
                "gpu_vs_cpu_min_cos": round(cos, 9)}
 

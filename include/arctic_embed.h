@@ -108,10 +108,18 @@ int ae_embed_batch_tokens(const ae_engine* e, ae_workspace* ws, const uint16_t* 
  * inputs: ids_dev[total_tokens] u16, cu_seqlens_dev[n_seqs+1] i32 (each sequence
  * 1..max_seq_len tokens; max_seq_len <= 512, 0 means 512), out_dev[n_seqs*384]
  * f32.  Asynchronous on `stream`; no host copies.  Used when the caller keeps
- * token ids in HBM. */
+ * token ids in HBM.  The device checks cu_seqlens (cu[0] = 0, cu[n_seqs] =
+ * total_tokens, every segment 1..max_seq_len tokens); a batch that fails is
+ * reported as AE_ERR_INVALID_ARG by the next ae_workspace_synchronize (its
+ * outputs are then unspecified, but every access stays in bounds). */
 int ae_forward_packed_device(const ae_engine* e, ae_workspace* ws, const uint16_t* ids_dev,
                              const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
                              int max_seq_len, float* out_dev, void* stream);
+/* Waits for the workspace's work on `stream` (NULL: its own stream) and reports
+ * the device-side batch checks of the asynchronous calls since the last one:
+ * AE_OK, or AE_ERR_INVALID_ARG (and the check is reset).  No counterpart in the
+ * reference, whose calls are all synchronous and panic on bad input. */
+int ae_workspace_synchronize(ae_workspace* ws, void* stream);
 
 /* ---- latency mode: one sequence at a time ------------------------------- */
 /* ParallelContext::new(n_threads) (src/parallel.rs:144-160): n_threads is clamped
@@ -180,9 +188,27 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
  * column over all total_tokens rows, integer scores, the exact-range int16
  * softmax (round(16383 * 2^(s - max)), exp2 in log2 units) and integer P @ V.
  * Bit-identical to that path; within a cosine budget of ae_attention_varlen.
- * Same arguments and synchronization as ae_attention_varlen. */
+ * Same arguments and synchronization as ae_attention_varlen, except that the V
+ * scales span every row: cu_seqlens must be an exact prefix sum (cu[0] = 0,
+ * cu[n_seqs] = total_tokens) of segments of at most 512 tokens, else
+ * AE_ERR_INVALID_ARG. */
 int ae_attention_varlen_quantized(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
                                   int total_tokens, float* ctx_dev, void* stream);
+/* ae_attention_varlen / ae_attention_varlen_quantized on a workspace's scratch,
+ * for callers that run the operator per layer (the reference's per-layer
+ * attention call, src/model.rs:607-694): asynchronous on `stream` (NULL: the
+ * workspace's), no host copy, no synchronization, no allocation (the quantized
+ * variant allocates its scratch on its first call, as
+ * ae_workspace_set_attention_mode does).  The caller states max_seq_len
+ * (1..512), the longest segment; n_seqs and total_tokens within the workspace
+ * capacity (AE_ERR_CAPACITY otherwise).  A cu_seqlens that is not an exact
+ * prefix sum of segments of 1..max_seq_len tokens is reported by the next
+ * ae_workspace_synchronize. */
+int ae_workspace_attention_varlen(ae_workspace* ws, const float* qkv_dev, const int32_t* cu_seqlens_dev,
+                                  int n_seqs, int total_tokens, int max_seq_len, float* ctx_dev, void* stream);
+int ae_workspace_attention_varlen_quantized(ae_workspace* ws, const float* qkv_dev, const int32_t* cu_seqlens_dev,
+                                            int n_seqs, int total_tokens, int max_seq_len, float* ctx_dev,
+                                            void* stream);
 
 /* ---- tools and test hooks (no counterpart in the reference) -------------- */
 /* Writes a seeded synthetic model in `.ae8` layout (fp32
@@ -211,11 +237,12 @@ int ae_workspace_set_timing(ae_workspace* ws, int enabled);
 int ae_workspace_set_graphs(ae_workspace* ws, int enabled);
 /* Attention of layers 0-10 in this workspace's forward passes.
  * AE_ATTENTION_EXACT (default): the reference's scalar order, bit-exact.
- * AE_ATTENTION_QUANTIZED: what the reference's ArmSme backend computes
- * (SimdBackend::ArmSme in src/model.rs:591-621 and :223-247: int8 Q, K, V and
- * int16 P, see ae_attention_varlen_quantized) for batches of at least 32 packed
- * tokens, or 16 for a single sequence; smaller batches keep the exact path.
- * Setting it the first time allocates the mode's scratch for max_tokens rows. */
+ * AE_ATTENTION_QUANTIZED: each sequence as the reference's forward_cls runs it
+ * on its ArmSme backend (src/model.rs:223-259): from 16 tokens on the quantized
+ * attention (int8 Q, K, V and int16 P, see ae_attention_varlen_quantized) with
+ * V scales over that sequence alone, below 16 tokens the exact path.  A
+ * sequence's result is therefore the same alone or in any batch.  Setting it
+ * the first time allocates the mode's scratch for the workspace capacity. */
 #define AE_ATTENTION_EXACT 0
 #define AE_ATTENTION_QUANTIZED 1
 int ae_workspace_set_attention_mode(ae_workspace* ws, int mode);

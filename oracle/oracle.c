@@ -375,6 +375,8 @@ typedef struct {
   const int* seg_start; /* [B] */
   const int* seg_len;   /* [B] */
   int sme;              /* attention of the reference's ArmSme backend (or_attention_sme) */
+  int pert_layer;       /* test hook: 1 + the layer whose input act_q gets pert_row/pert_col moved by one step */
+  int pert_row, pert_col;
   float *hidden, *tmp, *qkv, *ctx, *inter;
   int8_t *act_q, *inter_q;
   float* act_scale;
@@ -402,13 +404,28 @@ static void full_layer(const or_model* m, int l, fwd_ws* w, int quant_next, cons
   /* one layer over all T rows: src/model.rs:593-767 */
   const or_layer* L = &m->layers[l];
   const int T = w->T;
+  if (w->pert_layer == l + 1) { /* test hook: one int8 activation one step off */
+    int8_t* q = &w->act_q[(size_t)w->pert_row * H + w->pert_col];
+    *q = (int8_t)(*q < 127 ? *q + 1 : *q - 1);
+  }
   K->gemm(T, w->act_q, w->act_scale, &L->qkv, NULL, w->qkv);
-  if (w->sme && T >= (w->B == 1 ? 16 : 32)) { /* src/model.rs:607-621 (:245 for one sequence) */
-    int* cu = (int*)malloc(sizeof(int) * (w->B + 1));
-    for (int b = 0; b < w->B; b++) cu[b] = w->seg_start[b];
-    cu[w->B] = T;
-    or_attention_sme(w->qkv, T, cu, w->B, w->ctx);
-    free(cu);
+  if (w->sme) {
+    /* each sequence as forward_cls computes it on the ArmSme backend
+       (src/model.rs:244-259): the quantized attention over that sequence alone
+       (its own V column scales) from 16 tokens on, the exact path below */
+    for (int b = 0; b < w->B; b++) {
+      const int s0 = w->seg_start[b], len = w->seg_len[b];
+      if (len >= 16) {
+        const int cu[2] = {0, len};
+        or_attention_sme(w->qkv + (size_t)s0 * 3 * H, len, cu, 1, w->ctx + (size_t)s0 * H);
+      } else {
+        for (int h = 0; h < OR_HEADS; h++) {
+          const int ho = h * 32;
+          attention_head_k(w->qkv + (size_t)s0 * 3 * H, len, 3 * H, ho, H + ho, 2 * H + ho,
+                           w->ctx + (size_t)s0 * H + ho, H, K);
+        }
+      }
+    }
   } else {
     for (int b = 0; b < w->B; b++)
       for (int h = 0; h < OR_HEADS; h++) {
@@ -514,8 +531,13 @@ static void fwd_free(fwd_ws* w) {
 }
 
 /* runs one packed batch of B segments (already truncated) */
+typedef struct {
+  int sme;                       /* fwd_ws.sme */
+  int pert_layer, pert_row, pert_col; /* fwd_ws.pert_* */
+} fwd_opts;
+
 static int forward_packed_k(const or_model* m, const uint16_t* const* seq_ids, const int* lens, int B,
-                            int prune, float* out, const or_kernels* K) {
+                            int prune, float* out, const or_kernels* K, const fwd_opts* o) {
   int* starts = (int*)malloc(sizeof(int) * (B > 0 ? B : 1));
   int T = 0;
   for (int b = 0; b < B; b++) {
@@ -527,6 +549,12 @@ static int forward_packed_k(const or_model* m, const uint16_t* const* seq_ids, c
   }
   fwd_ws w = {0};
   w.T = T; w.B = B; w.seg_start = starts; w.seg_len = lens;
+  if (o) {
+    w.sme = o->sme;
+    w.pert_layer = o->pert_layer;
+    w.pert_row = o->pert_row;
+    w.pert_col = o->pert_col;
+  }
   if (fwd_alloc(&w, T)) { fwd_free(&w); free(starts); return OR_ERR_ARG; }
   embed_tokens(m, seq_ids, &w, K);
   for (int l = 0; l < OR_LAYERS - 1; l++) full_layer(m, l, &w, 1, K);
@@ -568,14 +596,14 @@ static int forward_packed_k(const or_model* m, const uint16_t* const* seq_ids, c
 
 static int forward_packed(const or_model* m, const uint16_t* const* seq_ids, const int* lens, int B,
                           int prune, float* out) {
-  return forward_packed_k(m, seq_ids, lens, B, prune, out, &or_scalar_kernels);
+  return forward_packed_k(m, seq_ids, lens, B, prune, out, &or_scalar_kernels, NULL);
 }
 
 static int forward_cls_k(const or_model* m, const uint16_t* ids, size_t n, float* out384, const or_kernels* K) {
   /* src/model.rs:191-192: seq_len = min(len, 512); empty input is rejected */
   int len = (int)(n < OR_MAX_POS ? n : OR_MAX_POS);
   if (len < 1) return OR_ERR_ARG;
-  return forward_packed_k(m, &ids, &len, 1, 1, out384, K);
+  return forward_packed_k(m, &ids, &len, 1, 1, out384, K, NULL);
 }
 
 int or_forward_cls(const or_model* m, const uint16_t* ids, size_t n, float* out384) {
@@ -604,7 +632,7 @@ static int forward_ragged_cls_k(const or_model* m, const uint16_t* ids, const ui
     seqs[i] = ids + offsets[i];
     cursor += lens[i];
   }
-  return forward_packed_k(m, seqs, lens, b, 1, out, K);
+  return forward_packed_k(m, seqs, lens, b, 1, out, K, NULL);
 }
 
 int or_forward_ragged_cls(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
@@ -623,6 +651,36 @@ int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offset
 int or_run_prefix_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
                       int upto_layer, float* hidden, int8_t* act_q, float* act_scale) {
   return run_prefix(m, ids, offsets, b, upto_layer, hidden, act_q, act_scale, 1);
+}
+
+int or_forward_cls_perturbed(const or_model* m, const uint16_t* ids, size_t n, int layer, int row, int col,
+                             float* out384) {
+  /* forward_cls with act_q[row][col] one step off (+1, or -1 at 127) at the
+     input of encoder layer `layer`: the sensitivity of the model to one int8
+     activation */
+  const int len = (int)(n > OR_MAX_POS ? OR_MAX_POS : n);
+  if (len < 1 || layer < 0 || layer > OR_LAYERS - 2 || row < 0 || row >= len || col < 0 || col >= H) return OR_ERR_ARG;
+  const fwd_opts o = {0, layer + 1, row, col};
+  return forward_packed_k(m, &ids, &len, 1, 1, out384, &or_scalar_kernels, &o);
+}
+
+int or_embed_tokens_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b, float* out) {
+  /* forward_cls (src/model.rs:185-513) of each sequence on the ArmSme backend,
+     run as one packed batch: every layer acts per sequence (full_layer's sme
+     branch), so each output equals that sequence's own forward_cls */
+  if (b < 1) return OR_ERR_ARG;
+  const uint16_t** seqs = (const uint16_t**)malloc(sizeof(void*) * b);
+  int* lens = (int*)malloc(sizeof(int) * b);
+  for (int i = 0; i < b; i++) {
+    int len = (int)(offsets[i + 1] - offsets[i]);
+    lens[i] = len > OR_MAX_POS ? OR_MAX_POS : len; /* src/model.rs:191 */
+    seqs[i] = ids + offsets[i];
+  }
+  const fwd_opts o = {1, 0, 0, 0};
+  const int rc = forward_packed_k(m, seqs, lens, b, 1, out, &or_scalar_kernels, &o);
+  free(seqs);
+  free(lens);
+  return rc;
 }
 
 static int run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b, int upto_layer,

@@ -185,10 +185,19 @@ int or_embed_batch_tokens(const or_model* m, const uint16_t* ids, const uint32_t
    and layers [0, upto_layer) and returns hidden/act_q/act_scale at that point. */
 int or_run_prefix(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
                   int upto_layer, float* hidden, int8_t* act_q, float* act_scale);
-/* or_run_prefix with the ArmSme backend's quantized attention in layers 0-10
-   (or_attention_sme for >= 32 packed tokens, >= 16 for one sequence) */
+/* or_run_prefix with the ArmSme backend's quantized attention in layers 0-10,
+   per sequence as forward_cls runs it (src/model.rs:244-259): or_attention_sme
+   over the sequence alone when it has >= 16 tokens, the exact attention below */
 int or_run_prefix_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b,
                       int upto_layer, float* hidden, int8_t* act_q, float* act_scale);
+/* test hook: forward_cls with act_q[row][col] moved one int8 step (+1, or -1 at
+   127) at the input of encoder layer `layer` (0..10) */
+int or_forward_cls_perturbed(const or_model* m, const uint16_t* ids, size_t n, int layer, int row, int col,
+                             float* out384);
+/* the whole forward_cls of each of the b sequences (offsets[b+1], each truncated
+   to 512) with the ArmSme backend's attention as or_run_prefix_sme applies it;
+   out [b, 384] */
+int or_embed_tokens_sme(const or_model* m, const uint16_t* ids, const uint32_t* offsets, int b, float* out);
 
 #ifdef __cplusplus
 }

@@ -80,6 +80,9 @@ _sigs = {
     "or_x86_embed_batch_tokens": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_size_t, ctypes.c_int, _vp]),
     "or_run_prefix": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
     "or_run_prefix_sme": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
+    "or_embed_tokens_sme": (ctypes.c_int, [_MP, _vp, _vp, ctypes.c_int, _vp]),
+    "or_forward_cls_perturbed": (ctypes.c_int, [_MP, _vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                _vp]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(_lib, _n)
@@ -196,6 +199,16 @@ class OracleModel:
             raise ValueError("or_forward_cls: %d" % rc)
         return out
 
+    def forward_cls_perturbed(self, ids, layer, row, col):
+        """forward_cls with act_q[row][col] one int8 step off at the input of encoder layer `layer`."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint16)
+        out = np.zeros(H, dtype=np.float32)
+        rc = _lib.or_forward_cls_perturbed(self._m, ids.ctypes.data, ids.size, int(layer), int(row), int(col),
+                                           out.ctypes.data)
+        if rc:
+            raise ValueError("or_forward_cls_perturbed: %d" % rc)
+        return out
+
     def forward_cls_unpruned(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.uint16)
         out = np.zeros(H, dtype=np.float32)
@@ -235,6 +248,15 @@ class OracleModel:
                                             out.ctypes.data)
         if rc:
             raise ValueError("or_x86_embed_batch_tokens: %d" % rc)
+        return out
+
+    def embed_tokens_sme(self, seqs):
+        """forward_cls of every sequence with the ArmSme backend's quantized attention (>= 16 tokens)."""
+        ids, offs = _pack(seqs)
+        out = np.zeros((len(seqs), H), dtype=np.float32)
+        rc = _lib.or_embed_tokens_sme(self._m, ids.ctypes.data, offs.ctypes.data, len(seqs), out.ctypes.data)
+        if rc:
+            raise ValueError("or_embed_tokens_sme: %d" % rc)
         return out
 
     def run_prefix_sme(self, seqs, upto_layer):

@@ -66,6 +66,9 @@ _SIGS = {
     "ae_gelu_smooth_quantize": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ae_attention_varlen": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "ae_attention_varlen_quantized": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "ae_workspace_attention_varlen": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "ae_workspace_attention_varlen_quantized": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "ae_workspace_synchronize": (_i32, [_vp, _vp]),
     "ae_write_synthetic_ae8": (_i32, [_c.c_char_p, _u64]),
     "ae_tokenizer_open": (_i32, [_c.c_char_p, _c.POINTER(_vp)]),
     "ae_tokenizer_close": (None, [_vp]),
@@ -324,6 +327,17 @@ class Workspace:
     def set_attention_mode(self, quantized):
         """Layers 0-10 with the reference's ArmSme quantized attention (True) or the exact path."""
         _check(_lib.ae_workspace_set_attention_mode(self._h, 1 if quantized else 0))
+
+    def synchronize(self, stream=None):
+        """Waits for the workspace's work and raises AeError (AE_ERR_INVALID_ARG) if a device-resident
+        batch since the last call failed its checks."""
+        _check(_lib.ae_workspace_synchronize(self._h, stream))
+
+    def attention_varlen(self, qkv_ptr, cu_ptr, n_seqs, total_tokens, max_seq_len, ctx_ptr, stream=None,
+                         quantized=False):
+        """ae_attention_varlen(_quantized) on this workspace's scratch: asynchronous, no allocation."""
+        fn = _lib.ae_workspace_attention_varlen_quantized if quantized else _lib.ae_workspace_attention_varlen
+        _check(fn(self._h, qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), int(max_seq_len), ctx_ptr, stream))
 
     def kernel_times(self):
         """{kind: (total_ms, launches)} since timing was enabled (synchronize first)."""

@@ -501,6 +501,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
   const int item = xcd_contiguous(blockIdx.x, p.B * 12);
   const int h = item / p.B, b = item - h * p.B;
   const int s0 = p.cu[b];
+  if (p.skip_from > 0 && p.cu[b + 1] - s0 >= p.skip_from) return;  // another kernel's segment
   const int L = min(p.cu[b + 1] - s0, 16 * NKB);
   const int lane = threadIdx.x & 63, q0 = (threadIdx.x >> 6) * 16;
   if (q0 >= L) return;  // wave-uniform; nothing below synchronizes across waves
@@ -679,6 +680,13 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
     hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
   else
     hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
+}
+
+void launch_attention_short(const AttnArgs& p, hipStream_t st) {
+  if (p.B <= 0) return;
+  AttnArgs q = p;
+  q.skip_from = 16;
+  hipLaunchKernelGGL(attention_rows_kernel<1>, dim3(p.B * 12), dim3(64), 0, st, q);
 }
 
 // ---------------------------------------------------------------------------

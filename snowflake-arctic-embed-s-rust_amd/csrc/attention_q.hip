@@ -86,10 +86,11 @@ __device__ __forceinline__ int exp2_q16(float x) {
 }  // namespace
 
 // Q and K of every token and head to int8 with their scales, and the per-column
-// |V| maximum over the batch folded into s.vmax (atomicMax on f32 bits; the
-// buffer is preset to bits(1e-8f), the reference's starting value).
+// |V| maximum folded into s.vmax (atomicMax on f32 bits; the buffer is preset to
+// bits(1e-8f), the reference's starting value): one maximum per column over the
+// whole batch, or (s.per_seq) one per sequence and column, vmax[b][c].
 // 64 tokens per workgroup of 12 waves.
-__global__ __launch_bounds__(768) void sme_pack_kernel(const float* qkv, int T, SmeArgs s) {
+__global__ __launch_bounds__(768) void sme_pack_kernel(const float* qkv, const int* cu, int B, int T, SmeArgs s) {
   const int tid = threadIdx.x, t0 = blockIdx.x * 64;
   const float k_mul = kInvSqrtD * 1.44269504088896340736f;  // inv_sqrt_d * LOG2_E in f32
   for (int it = tid; it < 64 * 12; it += 768) {  // one (token, head) per thread
@@ -101,40 +102,51 @@ __global__ __launch_bounds__(768) void sme_pack_kernel(const float* qkv, int T, 
     }
   }
   __shared__ float s_m[12][H];
-  {  // wave w: tokens t0 + w + 12i; lane: columns lane + 64k (row-contiguous loads)
-    const int w = tid >> 6, lane = tid & 63, n = min(64, T - t0);
+  // The block's tokens in runs that share one V scale group: the whole block,
+  // or (per_seq) its run inside each segment.  Wave w: tokens a + w + 12i of a
+  // run; lane: columns lane + 64k (row-contiguous loads).  Block-uniform loop.
+  const int w = tid >> 6, lane = tid & 63, t1 = min(T, t0 + 64);
+  int a = t0, g = s.per_seq ? find_segment(cu, B, t0) : 0;
+  while (a < t1 && g < (s.per_seq ? B : 1)) {
+    const int e = s.per_seq ? max(a, min(t1, cu[g + 1])) : t1;
     float m[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = w; i < n; i += 12) {
-      const float* vr = qkv + (size_t)(t0 + i) * HQKV + 2 * H + lane;
+    for (int t = a + w; t < e; t += 12) {
+      const float* vr = qkv + (size_t)t * HQKV + 2 * H + lane;
 #pragma unroll
       for (int k = 0; k < 6; k++) m[k] = vmax(m[k], fabsf(vr[64 * k]));
     }
 #pragma unroll
     for (int k = 0; k < 6; k++) s_m[w][lane + 64 * k] = m[k];
-  }
-  __syncthreads();
-  for (int c = tid; c < H; c += 768) {
-    float m = s_m[0][c];
+    __syncthreads();
+    if (e > a) {
+      for (int c = tid; c < H; c += 768) {
+        float mm = s_m[0][c];
 #pragma unroll
-    for (int w = 1; w < 12; w++) m = vmax(m, s_m[w][c]);
-    atomicMax(&s.vmax[c], __float_as_uint(m));
+        for (int v = 1; v < 12; v++) mm = vmax(mm, s_m[v][c]);
+        atomicMax(&s.vmax[(size_t)g * H + c], __float_as_uint(mm));
+      }
+    }
+    __syncthreads();
+    a = e;
+    g++;
   }
 }
 
-// V to int8 with the batch's per-column scales (quantize_v_row_neon), stored
-// transposed: s.vt[c][round8(cu[b] + 7b) + (t - cu[b])] for token t of segment b.
-// Workgroup (64-token block, head): the block's V columns are staged in LDS so
-// that both the f32 reads and the int8 writes are row-contiguous.
+// V to int8 with its group's per-column scales (quantize_v_row_neon: v *
+// (127 / vmax), the scale group being the batch or, per_seq, the sequence),
+// stored transposed: s.vt[c][round8(cu[b] + 7b) + (t - cu[b])] for token t of
+// segment b.  Workgroup (64-token block, head): the block's V columns are staged
+// in LDS so that both the f32 reads and the int8 writes are row-contiguous.
 __global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const int* cu, int B, int T, SmeArgs s,
                                                          size_t vt_len) {
   __shared__ float sv[64][33];
-  __shared__ float s_inv[32];
   __shared__ size_t s_pos[64];
+  __shared__ int s_grp[64];
   const int tid = threadIdx.x, t0 = blockIdx.x * 64, h = blockIdx.y;
-  if (tid < 32) s_inv[tid] = 127.0f / __uint_as_float(s.vmax[h * 32 + tid]);
-  if (tid >= 64 && tid < 128 && t0 + tid - 64 < T) {
-    const int t = t0 + tid - 64, b = find_segment(cu, B, t);
-    s_pos[tid - 64] = (size_t)((cu[b] + 7 * b + 7) & ~7) + (size_t)(t - cu[b]);
+  if (tid < 64) {
+    const int t = min(t0 + tid, T - 1), b = find_segment(cu, B, t);
+    s_pos[tid] = (size_t)((cu[b] + 7 * b + 7) & ~7) + (size_t)(t - cu[b]);
+    s_grp[tid] = s.per_seq ? b : 0;
   }
   for (int i = tid; i < 64 * 32; i += 256) {
     const int r = i >> 5, c = i & 31;
@@ -143,7 +155,10 @@ __global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const
   __syncthreads();
   for (int i = tid; i < 64 * 32; i += 256) {
     const int c = i >> 6, r = i & 63, t = t0 + r;
-    if (t < T) s.vt[(size_t)(h * 32 + c) * vt_len + s_pos[r]] = (int8_t)sat8(cvtn(sv[r][c] * s_inv[c]));
+    if (t < T) {
+      const float inv = 127.0f / __uint_as_float(s.vmax[(size_t)s_grp[r] * H + h * 32 + c]);
+      s.vt[(size_t)(h * 32 + c) * vt_len + s_pos[r]] = (int8_t)sat8(cvtn(sv[r][c] * inv));
+    }
   }
 }
 
@@ -159,16 +174,19 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   const int h = item / max_tiles, tile = item - h * max_tiles;
   const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
   const int nq = rec.w;
-  if (nq == 0) return;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;
+  // per_seq: sequences under 16 tokens take the exact attention (forward_cls,
+  // src/model.rs:244-259), launched separately
+  if (nq == 0 || (sa.per_seq && L < 16)) return;
   const int pitch16 = sme_p_pitch(p.s_pitch);
   int16_t* P = reinterpret_cast<int16_t*>(smem);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const ExpTab tb = exp_tab_regs();
+  const int b = find_segment(p.cu, p.B, s0);
   if (tid < 32) {
-    const float vm = __uint_as_float(sa.vmax[h * 32 + tid]);
+    const float vm = __uint_as_float(sa.vmax[(size_t)(sa.per_seq ? b : 0) * H + h * 32 + tid]);
     s_vscale[tid] = vm * (1.0f / 127.0f);
     s_isum[tid] = 0;
   }
@@ -180,7 +198,6 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
   const int nch = (L + 31) >> 5;
   v_i64 vb[16];
   {
-    const int b = find_segment(p.cu, p.B, s0);
     const int8_t* vrow =
         sa.vt + (size_t)(h * 32 + 16 * (wave & 1) + lr) * vt_len + ((p.cu[b] + 7 * b + 7) & ~7) + 8 * lg;
 #pragma unroll
@@ -374,8 +391,8 @@ __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs 
 
 void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan) {
   if (T <= 0 || p.B <= 0) return;
-  launch_fill_u32(s.vmax, H, 0x322bcc77u, st);  // bits of 1e-8f
-  hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(768), 0, st, p.qkv, T, s);
+  launch_fill_u32(s.vmax, H * (s.per_seq ? p.B : 1), 0x322bcc77u, st);  // bits of 1e-8f
+  hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(768), 0, st, p.qkv, p.cu, p.B, T, s);
   const size_t vt_len = sme_vt_len(T, p.B);
   hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
   if (plan) launch_attention_plan(p, T, st);

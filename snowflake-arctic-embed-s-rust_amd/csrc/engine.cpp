@@ -146,6 +146,7 @@ struct ae_workspace {
   // ArmSme attention in layers 0-10; its scratch is allocated when the mode is set
   int attention_mode = AE_ATTENTION_EXACT;
   aek::SmeArgs sme{};
+  int* err = nullptr;        // device error word: bit 0 = a packed batch with a bad segment (ae_workspace_synchronize)
   int* splitk = nullptr;     // int32 partial sums of split-K GEMMs (small M)
   size_t splitk_ints = 0;
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
@@ -393,12 +394,19 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.q = ws->act_q;
     p.scale = ws->act_scale;
     p.rowmax_init = ws->rowmax_ctx;
+    p.max_len = max_len;
+    p.err = ws->err;
     launch_ln_quant(p, kLnSrcEmb, st);
   }
   const int s_pitch = attention_pitch(max_len);
-  // the reference's ArmSme backend takes its quantized attention from 32 packed
-  // tokens on (src/model.rs:608), or 16 for a single sequence (:245)
-  const bool sme = ws->attention_mode == AE_ATTENTION_QUANTIZED && T >= (B == 1 ? 16 : 32);
+  // AE_ATTENTION_QUANTIZED: every sequence as forward_cls runs it on the
+  // reference's ArmSme backend (src/model.rs:244-259): the quantized attention
+  // with that sequence's own V scales from 16 tokens on, the exact one below,
+  // so a sequence's result does not depend on its batch mates
+  const bool sme = ws->attention_mode == AE_ATTENTION_QUANTIZED && max_len >= 16;
+  if (sme && !ws->sme.vt) return fail(AE_ERR_INVALID_ARG, "quantized attention scratch missing");
+  SmeArgs sme_args = ws->sme;
+  sme_args.per_seq = 1;
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
     const DevLayer& D = E->layers[l];
@@ -409,10 +417,12 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
-      if (sme)
-        launch_attention_sme(a, ws->sme, T, st, /*plan=*/l == 0);
-      else
+      if (sme) {
+        launch_attention_sme(a, sme_args, T, st, /*plan=*/l == 0);
+        launch_attention_short(a, st);
+      } else {
         launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
+      }
     }
     gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1,
                  gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
@@ -588,6 +598,37 @@ int check_ids(const uint16_t* ids, size_t n) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The quantized attention's scratch for the workspace capacity (int8 Q and K,
+// their scales, the |V| column maxima per sequence and the transposed int8 V),
+// allocated once.  All-or-nothing: on a failed allocation the ones already made
+// are freed and ws->sme stays empty.
+int alloc_sme_scratch(ae_workspace* ws) {
+  if (ws->sme.vt) return AE_OK;
+  HIP_TRY(hipSetDevice(ws->e->device));
+  const size_t T = size_t(ws->max_tokens), B = size_t(ws->max_seqs);
+  const size_t bytes[6] = {T * 384, T * 384, T * 12 * 4, T * 12 * 4, B * 384 * 4,
+                           384 * aek::sme_vt_len(ws->max_tokens, ws->max_seqs)};
+  void* p[6] = {};
+  for (int i = 0; i < 6; i++) {
+    const hipError_t e = hipMalloc(&p[i], bytes[i]);
+    if (e != hipSuccess) {
+      for (int j = 0; j < i; j++) (void)hipFree(p[j]);
+      return fail(AE_ERR_HIP, std::string("quantized attention scratch: ") + hipGetErrorString(e));
+    }
+  }
+  for (void* q : p) ws->dev.push_back(q);
+  aek::SmeArgs s{};
+  s.q8 = static_cast<int8_t*>(p[0]);
+  s.k8 = static_cast<int8_t*>(p[1]);
+  s.qs = static_cast<float*>(p[2]);
+  s.ks = static_cast<float*>(p[3]);
+  s.vmax = static_cast<uint32_t*>(p[4]);
+  s.vt = static_cast<int8_t*>(p[5]);
+  aek::init_attention_sme_kernels();
+  ws->sme = s;
+  return AE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -666,7 +707,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
     return rc;
   };
   int rc;
-  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->attn_plan, aek::attention_plan_ints(int(B), int(T)))) ||
+  if ((rc = A(&ws->ids, T)) || (rc = A(&ws->cu, B + 1)) || (rc = A(&ws->err, size_t(1))) || (rc = A(&ws->attn_plan, aek::attention_plan_ints(int(B), int(T)))) ||
       (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
       (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
       (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
@@ -679,6 +720,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
   // is small enough to split; launch_gemm lowers the split count to fit
   ws->splitk_ints = std::min<size_t>(size_t(6) << 20, 3 * T * 1536);
   if ((rc = A(&ws->splitk, ws->splitk_ints))) return rc;
+  HIP_TRY(hipMemset(ws->err, 0, sizeof(int)));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_ids), T * sizeof(uint16_t), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_cu), (B + 1) * sizeof(int), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_out), B * 384 * sizeof(float), hipHostMallocDefault));
@@ -908,6 +950,12 @@ static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev,
     if (L < 0 || cu[b + 1] > total_tokens) return fail(AE_ERR_INVALID_ARG, "cu_seqlens is not a prefix sum of total_tokens");
     max_len = std::max(max_len, L);
   }
+  // The quantized path takes its V column scales over every row of the batch,
+  // so a row outside the segments, or cut from one, would still change them:
+  // it takes exact prefix sums of segments of at most 512 tokens.
+  if (quantized && (cu[0] != 0 || cu[n_seqs] != total_tokens || max_len > ae::kMaxPos))
+    return fail(AE_ERR_INVALID_ARG, "quantized attention needs cu_seqlens[0] = 0, cu_seqlens[n_seqs] = total_tokens "
+                                    "and segments of at most 512 tokens");
   int* plan = nullptr;
   HIP_TRY(hipMalloc(reinterpret_cast<void**>(&plan), aek::attention_plan_ints(n_seqs, total_tokens) * sizeof(int)));
   aek::init_attention_kernels();
@@ -935,6 +983,58 @@ static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev,
   (void)hipFree(plan);
   if (sme) (void)hipFree(sme);
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("attention: ") + hipGetErrorString(err));
+  return AE_OK;
+}
+
+// The same operators on the workspace's scratch: no allocation after the first
+// quantized call, no host copy, no synchronization.  The caller bounds the
+// segment lengths (max_seq_len, 1..512); a batch that breaks the bound, or whose
+// cu_seqlens is not a prefix sum of total_tokens, is reported by the next
+// ae_workspace_synchronize.
+static int workspace_attention(ae_workspace* ws, const float* qkv_dev, const int32_t* cu_dev, int n_seqs,
+                               int total_tokens, int max_seq_len, float* ctx_dev, void* stream, bool quantized) {
+  if (!ws || !qkv_dev || !cu_dev || !ctx_dev || n_seqs < 0 || total_tokens < n_seqs || max_seq_len < 1 ||
+      max_seq_len > ae::kMaxPos)
+    return fail(AE_ERR_INVALID_ARG, "bad attention arguments");
+  if (n_seqs == 0) return AE_OK;
+  if (n_seqs > ws->max_seqs || total_tokens > ws->max_tokens)
+    return fail(AE_ERR_CAPACITY, "attention batch exceeds workspace capacity");
+  HIP_TRY(hipSetDevice(ws->e->device));
+  if (quantized)
+    if (int rc = alloc_sme_scratch(ws)) return rc;
+  hipStream_t st = stream ? as_stream(stream) : ws->stream;
+  aek::launch_check_segments(cu_dev, n_seqs, total_tokens, max_seq_len, ws->err, st);
+  aek::AttnArgs a{qkv_dev, cu_dev, n_seqs, ws->attn_plan, ctx_dev, nullptr, nullptr, aek::attention_pitch(max_seq_len)};
+  if (quantized) aek::launch_attention_sme(a, ws->sme, total_tokens, st);  // per_seq = 0: the batch's V scales
+  else aek::launch_attention(a, total_tokens, st);
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
+int ae_workspace_attention_varlen(ae_workspace* ws, const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
+                                  int total_tokens, int max_seq_len, float* ctx_dev, void* stream) {
+  return workspace_attention(ws, qkv_dev, cu_seqlens_dev, n_seqs, total_tokens, max_seq_len, ctx_dev, stream, false);
+}
+
+int ae_workspace_attention_varlen_quantized(ae_workspace* ws, const float* qkv_dev, const int32_t* cu_seqlens_dev,
+                                            int n_seqs, int total_tokens, int max_seq_len, float* ctx_dev,
+                                            void* stream) {
+  return workspace_attention(ws, qkv_dev, cu_seqlens_dev, n_seqs, total_tokens, max_seq_len, ctx_dev, stream, true);
+}
+
+int ae_workspace_synchronize(ae_workspace* ws, void* stream) {
+  if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
+  HIP_TRY(hipSetDevice(ws->e->device));
+  hipStream_t st = stream ? as_stream(stream) : ws->stream;
+  HIP_TRY(hipStreamSynchronize(st));
+  if (st != ws->stream) HIP_TRY(hipStreamSynchronize(ws->stream));
+  int err = 0;
+  HIP_TRY(hipMemcpy(&err, ws->err, sizeof(int), hipMemcpyDeviceToHost));
+  if (err) {
+    HIP_TRY(hipMemset(ws->err, 0, sizeof(int)));
+    return fail(AE_ERR_INVALID_ARG, "a packed batch had a segment outside 1..max_seq_len tokens or cu_seqlens that "
+                                    "is not a prefix sum of total_tokens");
+  }
   return AE_OK;
 }
 
@@ -978,22 +1078,8 @@ int ae_workspace_set_attention_mode(ae_workspace* ws, int mode) {
   if (!ws) return fail(AE_ERR_INVALID_ARG, "null workspace");
   if (mode != AE_ATTENTION_EXACT && mode != AE_ATTENTION_QUANTIZED)
     return fail(AE_ERR_INVALID_ARG, "unknown attention mode");
-  if (mode == AE_ATTENTION_QUANTIZED && !ws->sme.vmax) {
-    HIP_TRY(hipSetDevice(ws->e->device));
-    const size_t T = size_t(ws->max_tokens);
-    int rc;
-    if ((rc = dalloc(&ws->sme.q8, T * 384)) || (rc = dalloc(&ws->sme.k8, T * 384)) || (rc = dalloc(&ws->sme.qs, T * 12)) ||
-        (rc = dalloc(&ws->sme.ks, T * 12)) || (rc = dalloc(&ws->sme.vmax, size_t(384))) ||
-        (rc = dalloc(&ws->sme.vt, 384 * aek::sme_vt_len(ws->max_tokens, ws->max_seqs))))
-      return rc;
-    ws->dev.push_back(ws->sme.q8);
-    ws->dev.push_back(ws->sme.k8);
-    ws->dev.push_back(ws->sme.qs);
-    ws->dev.push_back(ws->sme.ks);
-    ws->dev.push_back(ws->sme.vmax);
-    ws->dev.push_back(ws->sme.vt);
-    aek::init_attention_sme_kernels();
-  }
+  if (mode == AE_ATTENTION_QUANTIZED)
+    if (int rc = alloc_sme_scratch(ws)) return rc;
   ws->attention_mode = mode;
   return AE_OK;
 }

@@ -80,8 +80,14 @@ struct LnArgs {
   float* scale;     // [T]
   uint32_t* rowmax_init;   // optional: set to bits(1e-8f) for each row
   uint32_t* rowmax_init2;  // optional second buffer
+  // kLnSrcEmb, optional: bit 0 of *err is set when cu is not a prefix sum of T
+  // with every segment 1..max_len tokens long (rows are still clamped in bounds)
+  int max_len;
+  int* err;
 };
 void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st);
+// bit 0 of *err when cu[0..B] is not a prefix sum of T with segments of 1..max_len tokens
+void launch_check_segments(const int* cu, int B, int T, int max_len, int* err, hipStream_t st);
 // An N = 384 GEMM (kEpiF32) followed by the LayerNorm + SmoothQuant of its
 // output rows (ln.src is ignored: the GEMM output).  With split K the LayerNorm
 // runs in the split-K epilogue and p.out is not written; otherwise the GEMM
@@ -102,6 +108,7 @@ struct AttnArgs {
   const float* smooth;     // attn_out inv_smooth [384] or null
   uint32_t* rowmax;        // [T] or null
   int s_pitch;             // score row pitch: attention_pitch(max sequence length)
+  int skip_from = 0;       // attention_rows_kernel: segments of at least this many tokens are left out (0: none)
 };
 int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
@@ -124,11 +131,17 @@ struct SmeArgs {
   uint32_t* vmax;   // [384], f32 bits
   int8_t* vt;       // [384][sme_vt_len(T, B)]: int8 V per head column, keys contiguous; segment b
                     // starts at round8(cu[b] + 7b), so every 8-key group is 8-byte aligned
+  // 0: V column scales over the whole packed batch (vmax [384]), every segment
+  // quantized; 1: per sequence as forward_cls runs it (vmax [B][384]), segments
+  // of fewer than 16 tokens left to the exact attention (launch_attention_short)
+  int per_seq = 0;
 };
 inline size_t sme_vt_len(int T, int B) { return ((size_t)T + 7 * (size_t)B + 64 + 7) & ~(size_t)7; }
 // the packing, the plan (plan = true) and the attention; p.smooth / p.rowmax as launch_attention
 void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_t st, bool plan = true);
 void init_attention_sme_kernels();  // once per device before the first launch
+// the exact attention of the segments shorter than 16 tokens only (the rest untouched)
+void launch_attention_short(const AttnArgs& p, hipStream_t st);
 // test hook: raw results of the exact-product MFMA (16 floats per lane per set of 64 pairs)
 void launch_mfma_products(const float* a, const float* b, float* out, int n_sets, hipStream_t st);
 

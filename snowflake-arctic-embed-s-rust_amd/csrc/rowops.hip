@@ -21,6 +21,17 @@ namespace aek {
 constexpr int kLnRows = 32;
 constexpr int kLnPitch = 388;
 
+// bit 0 of *err when cu[0..B] is not a prefix sum of T with every segment
+// 1..max_len tokens long; run by the 256 threads of one workgroup
+__device__ __forceinline__ void check_segments(const int* cu, int B, int T, int max_len, int* err) {
+  bool bad = threadIdx.x == 0 && (cu[0] != 0 || cu[B] != T);
+  for (int b = threadIdx.x; b < B; b += 256) {
+    const int len = cu[b + 1] - cu[b];
+    bad = bad || len < 1 || len > max_len;
+  }
+  if (bad) atomicOr(err, 1);
+}
+
 // LAT (few rows: latency, not bandwidth, bounds the launch): gamma, beta and
 // inv_smooth are loaded into registers at the start instead of after the sums.
 template <int SRC, bool LAT>
@@ -43,6 +54,9 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   const int rrow = valid ? row : p.T - 1;
 
   float4 xv[12];
+  // a device-resident batch is checked by the first workgroup (segments longer
+  // than max_len would leave rows without attention)
+  if (SRC == kLnSrcEmb && p.err && blockIdx.x == 0) check_segments(p.cu, p.B, p.T, p.max_len, p.err);
   if (SRC == kLnSrcEmb) {
     // ids and positions are validated on the host; the clamps keep a malformed
     // device-resident batch inside the tables
@@ -130,6 +144,13 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
       if (p.rowmax_init2) p.rowmax_init2[row] = __float_as_uint(1e-8f);
     }
   }
+}
+
+__global__ __launch_bounds__(256) void check_segments_kernel(const int* cu, int B, int T, int max_len, int* err) {
+  check_segments(cu, B, T, max_len, err);
+}
+void launch_check_segments(const int* cu, int B, int T, int max_len, int* err, hipStream_t st) {
+  if (B > 0) hipLaunchKernelGGL(check_segments_kernel, dim3(1), dim3(256), 0, st, cu, B, T, max_len, err);
 }
 
 // up to this many workgroups (a small fraction of the GPU) the launch is

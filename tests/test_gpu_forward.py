@@ -114,6 +114,49 @@ def test_text_api(engine, ws):
     assert engine.embed_batch(ws, []).shape == (0, 384)
 
 
+def test_text_api_reference_fixtures(engine, ws, oracle_model):
+    """The text front end on the reference's own id records (tests/accuracy_test.rs:86-96,
+    tests/long_accuracy_test.rs:45-71): the tokenizer reproduces all 19 id lists, and
+    embed_query / embed_document / embed_batch on the texts equal the oracle's forward_cls of the
+    recorded ids, bit for bit."""
+    d = json.load(open(os.path.join(GOLDEN, "tokenizer_vectors.json"), encoding="utf-8"))
+    tok = ae.Tokenizer(os.path.join(GOLDEN, "vocab.txt"))
+    texts, refs = [], []
+    for r in d["short"]:
+        q = r["kind"] == "query"
+        ids = tok.encode_query(r["raw_text"]) if q else tok.encode(r["raw_text"])
+        assert list(ids) == r["ids"], r["raw_text"]
+        emb = engine.embed_query(ws, r["raw_text"]) if q else engine.embed_document(ws, r["raw_text"])
+        ref = oracle_model.forward_cls(np.array(r["ids"], np.uint16))
+        assert np.array_equal(emb.view(np.uint32), ref.view(np.uint32)), r["raw_text"]
+        if not q:
+            texts.append(r["raw_text"])
+            refs.append(ref)
+    for r in d["long"]:
+        assert list(tok.encode(r["text"])) == r["ids"], r["name"]
+        emb = engine.embed_document(ws, r["text"])
+        ref = oracle_model.forward_cls(np.array(r["ids"], np.uint16))
+        assert np.array_equal(emb.view(np.uint32), ref.view(np.uint32)), r["name"]
+        texts.append(r["text"])
+        refs.append(ref)
+    batch = engine.embed_batch(ws, texts, is_query=False, num_threads=4)
+    assert np.array_equal(batch.view(np.uint32), np.stack(refs).view(np.uint32))
+
+
+def test_parallel_context_matches_oracle(engine, oracle_model):
+    """Latency mode at the lengths of the reference's tests/parallel_test.rs:9-51 (its ids): every
+    call of embed_tokens_parallel (eager, capture, replays) equals the oracle's forward_cls."""
+    par = engine.parallel_context(4)
+    for n in [1, 2, 5, 8, 15, 16, 17, 31, 33, 64, 100, 128, 257, 512]:
+        ids = np.array([101] + [1996 + (i * 37) % 5000 for i in range(max(0, n - 2))] + ([102] if n >= 2 else []),
+                       np.uint16)
+        ref = oracle_model.forward_cls(ids)
+        for call in range(3):
+            e = engine.embed_tokens_parallel(ids, par)
+            assert np.array_equal(e.view(np.uint32), ref.view(np.uint32)), (n, call)
+    par.close()
+
+
 def test_parallel_context_matches_workspace(engine, ws):
     """Latency mode (src/lib.rs:104-133) at the lengths and thread counts of the
     reference's tests/parallel_test.rs: embed_tokens_parallel equals embed_tokens bit
@@ -176,10 +219,17 @@ def test_kernel_timing(engine, ws):
     assert all(v[0] >= 0 for v in t.values())
 
 
+def oracle_threads():
+    """Host threads for the multithreaded oracle: the CPUs this process may use, at most the 16
+    a one-GPU job is given on the GPU box."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
 @pytest.mark.parametrize("cfg", ["c3", "c4", "c5"])
 def test_full_size_configs(engine, oracle_model, cfg):
-    """BASELINE configs[2..4] at full size: size-independent properties on every
-    row (unit norm, finite) and oracle parity on a sample of rows."""
+    """BASELINE configs[2..4] at full size in one packed device batch each: every row of C3
+    (256 x 16-512) and C4 (64 x 512), and 512 random rows of C5 (8192 x 8-64), bit-identical to
+    the oracle (its embed_batch over the host's cores); unit norm and finite on every row."""
     seqs = {"c3": lambda: ragged_batch(256, 16, 512, 3), "c4": lambda: ragged_batch(64, 512, 512, 4),
             "c5": lambda: ragged_batch(8192, 8, 64, 5)}[cfg]()
     T = sum(len(s) for s in seqs)
@@ -188,9 +238,12 @@ def test_full_size_configs(engine, oracle_model, cfg):
     big.close()
     assert np.all(np.isfinite(out))
     assert np.abs(np.linalg.norm(out.astype(np.float64), axis=1) - 1).max() < 1e-5
-    idx = np.random.default_rng(0).choice(len(seqs), 3 if cfg != "c5" else 24, replace=False)
-    ref = np.stack([oracle_model.forward_cls(seqs[i]) for i in idx])
-    check_close(out[idx], ref, cfg + " sample")
+    if cfg == "c5":
+        idx = np.sort(np.random.default_rng(0).choice(len(seqs), 512, replace=False))
+    else:
+        idx = np.arange(len(seqs))
+    ref = oracle_model.embed_batch_tokens([seqs[i] for i in idx], oracle_threads())
+    check_close(out[idx], ref, "%s: %d rows" % (cfg, len(idx)))
 
 
 @pytest.mark.parametrize("layers", [0, 1, 2, 11])
@@ -246,7 +299,8 @@ def ws_quant(engine):
 def test_quantized_attention_mode_prefix_state(engine, ws_quant, oracle_model, case):
     """Workspace in AE_ATTENTION_QUANTIZED mode: the state after the embedding and
     `layers` layers equals the oracle run with the ArmSme backend's attention in
-    layers 0-10 (>= 32 packed tokens, >= 16 for one sequence), bit for bit."""
+    layers 0-10 (per sequence: from 16 tokens on, with the sequence's own V scales;
+    ragged_l1 holds a 12-token sequence that keeps the exact path), bit for bit."""
     seqs, layers = {"ragged_l1": (ragged_batch(3, 5, 70, 17), 1), "ragged_l11": (ragged_batch(4, 3, 90, 19), 11),
                     "single16": (ragged_batch(1, 20, 20, 3), 2), "single_short": (ragged_batch(1, 12, 12, 3), 2),
                     "fused_ffn": (ragged_batch(10, 400, 512, 29), 1)}[case]
@@ -256,3 +310,55 @@ def test_quantized_attention_mode_prefix_state(engine, ws_quant, oracle_model, c
     if case == "ragged_l1":  # the mode changed the state: the exact path differs
         eh, _, _ = oracle_model.run_prefix(seqs, layers)
         assert not np.array_equal(h, eh)
+
+
+def test_quantized_attention_mode_full_forward_and_graphs(engine, oracle_model, torch_gpu):
+    """AE_ATTENTION_QUANTIZED through the whole forward pass (layer-11 tail included) on a
+    device-resident batch: eager, then graph capture, then replays (with other batches through the
+    workspace in between) all equal the oracle's per-sequence ArmSme forward_cls bit for bit; and a
+    sequence's embedding is the same alone as inside the batch."""
+    torch = torch_gpu
+    seqs = ragged_batch(7, 8, 300, 51) + [ragged_batch(1, 15, 15, 52)[0], ragged_batch(1, 16, 16, 53)[0]]
+    lens = [len(s) for s in seqs]
+    T, B = int(sum(lens)), len(seqs)
+    ref = oracle_model.embed_tokens_sme(seqs)
+    w = engine.workspace(4096, 64)
+    w.set_attention_mode(True)
+    ids = torch.from_numpy(np.concatenate(seqs).view(np.int16)).cuda()
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).cuda()
+    out = torch.zeros((B, 384), dtype=torch.float32, device="cuda")
+    for i in range(4):  # eager, capture, replay, replay
+        out.zero_()
+        torch.cuda.synchronize()
+        engine.forward_packed_device(w, ids.data_ptr(), cu.data_ptr(), B, T, out.data_ptr(), w.stream, max(lens))
+        w.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), i
+        engine.embed_batch_tokens(w, seqs[:3])  # other shapes in between
+    for i in (0, 6, 7, 8):
+        alone = engine.embed_tokens(w, seqs[i])
+        assert np.array_equal(alone.view(np.uint32), ref[i].view(np.uint32)), i
+    w.close()
+
+
+def test_device_batch_check_reports_long_segment(engine, torch_gpu):
+    """ae_forward_packed_device checks the device-resident cu_seqlens on the device: a segment
+    longer than the stated max_seq_len (every access still in bounds) is reported by the next
+    ae_workspace_synchronize, which then resets; a good batch afterwards reports nothing."""
+    torch = torch_gpu
+    w = engine.workspace(1024, 8)
+    seqs = ragged_batch(3, 20, 60, 61) + [ragged_batch(1, 100, 100, 62)[0]]
+    lens = [len(s) for s in seqs]
+    ids = torch.from_numpy(np.concatenate(seqs).view(np.int16)).cuda()
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).cuda()
+    out = torch.zeros((len(seqs), 384), dtype=torch.float32, device="cuda")
+    w.set_graphs(False)
+    engine.forward_packed_device(w, ids.data_ptr(), cu.data_ptr(), len(seqs), sum(lens), out.data_ptr(), w.stream, 64)
+    with pytest.raises(ae.AeError) as e:
+        w.synchronize()
+    assert e.value.code == ae.AE_ERR_INVALID_ARG
+    w.synchronize()  # reset
+    engine.forward_packed_device(w, ids.data_ptr(), cu.data_ptr(), len(seqs), sum(lens), out.data_ptr(), w.stream, 100)
+    w.synchronize()
+    assert np.array_equal(out.cpu().numpy(), engine.embed_batch_tokens(w, seqs))
+    w.close()

@@ -52,6 +52,37 @@ def test_gemm_bit_exact(torch_gpu, n, k, m, with_res):
     assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
 
 
+@pytest.mark.parametrize("k,n", [(384, 1152), (384, 384), (384, 1536), (1536, 384)])
+@pytest.mark.parametrize("m", [128, 4096, 32768])
+def test_gemm_configs1_microbench_shapes(torch_gpu, m, k, n):
+    """BASELINE configs[1] (the standalone W8A8 GEMM microbench that bench.py --gemm times) at its
+    own sizes and distributions: A int8 U[-127,127] with row scales U(0.01,0.1), W [K x N] int8
+    U[-127,127] (stored [N,K]) with column scales U(0.0002,0.0006), bias N(0,0.02), f32 out.
+    GEMM rows are independent, so every row at M = 128 and 64 rows otherwise (the first and
+    last 8 and 48 random ones) are checked bit for bit against the oracle's gemm_scalar_fused."""
+    torch = torch_gpu
+    rng = np.random.default_rng(1000 * m + n + k)
+    w = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(0.0002, 0.0006, n).astype(f32)
+    b = rng.normal(0, 0.02, n).astype(f32)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    lin = ae.Linear(w, ws, b, np.ones(k, f32))
+    a_d, sa_d = dev(torch, a), dev(torch, sa)
+    out_d = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    lin.gemm(m, a_d.data_ptr(), sa_d.data_ptr(), None, out_d.data_ptr())
+    torch.cuda.synchronize()
+    out = out_d.cpu().numpy()
+    lin.close()
+    if m <= 128:
+        rows = np.arange(m)
+    else:
+        rows = np.unique(np.concatenate([np.arange(8), np.arange(m - 8, m), rng.choice(m, 48, replace=False)]))
+    ref = orc.gemm(a[rows], sa[rows], w, ws, b)
+    assert np.array_equal(bits(out[rows]), bits(ref))
+    assert np.all(np.isfinite(out))
+
+
 def test_gemm_extreme_accumulators(torch_gpu):
     torch = torch_gpu
     n, k, m = 384, 1536, 3
@@ -336,3 +367,41 @@ def test_attention_bit_exact_extreme_magnitudes(torch_gpu, lens):
     torch.cuda.synchronize()
     ref = orc.attention(qkv, cu)
     assert np.array_equal(bits(ctx_d.cpu().numpy()), bits(ref))
+
+
+def test_workspace_attention_operators(torch_gpu, model_dir):
+    """The workspace-scratch attention operators (asynchronous, no allocation or host copy per
+    call) give the bits of the synchronous operators; the quantized operator refuses batches whose
+    V scales would include rows outside the segments (a segment over 512 tokens, or cu_seqlens not
+    ending at total_tokens) instead of cutting them."""
+    torch = torch_gpu
+    engine = ae.Engine.from_dir(str(model_dir))
+    w = engine.workspace(4096, 16)
+    lens = [1, 16, 33, 130, 512, 7, 64]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    rng = np.random.default_rng(71)
+    qkv = rng.normal(0, 1.0, (T, 1152)).astype(f32)
+    qkv_d, cu_d = dev(torch, qkv), dev(torch, cu)
+    for quantized in (False, True):
+        a = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+        b = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+        (ae.attention_varlen_quantized if quantized else ae.attention_varlen)(
+            qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, a.data_ptr())
+        for _ in range(2):
+            w.attention_varlen(qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, max(lens), b.data_ptr(),
+                               quantized=quantized)
+        w.synchronize()
+        assert np.array_equal(bits(a.cpu().numpy()), bits(b.cpu().numpy())), quantized
+    ctx = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+    for bad in ([0, 600, 700], [0, 16, 40]):  # 600 > 512; cu ends below total_tokens = 48
+        c = dev(torch, np.array(bad, np.int32))
+        with pytest.raises(ae.AeError) as e:
+            ae.attention_varlen_quantized(qkv_d.data_ptr(), c.data_ptr(), 2, bad[-1] if bad[-1] > 48 else 48,
+                                          ctx.data_ptr())
+        assert e.value.code == ae.AE_ERR_INVALID_ARG
+    with pytest.raises(ae.AeError) as e:  # more sequences than the workspace holds
+        w.attention_varlen(qkv_d.data_ptr(), cu_d.data_ptr(), 17, T, 512, ctx.data_ptr())
+    assert e.value.code == ae.AE_ERR_CAPACITY
+    w.close()
+    engine.close()
