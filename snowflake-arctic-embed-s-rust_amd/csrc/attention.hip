@@ -32,7 +32,8 @@ constexpr int kAttnQ = 32;     // queries per workgroup
 // whole assignment from one scalar load.  Tiles follow the packed segment order
 // (neighbouring tiles read neighbouring K/V rows); records past the last tile,
 // up to max_tiles, have nq = 0.  Rows past lmax (the score row length) get no
-// tiles.
+// tiles, and no record is written past max_tiles (a cu_seqlens that is not a
+// prefix sum of at most T tokens could ask for more).
 __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int max_tiles,
                                                              int4* plan) {
   __shared__ int part[256];
@@ -56,7 +57,8 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
   int at = tid == 0 ? 0 : part[tid];
   for (int b = b0; b < b1; b++) {
     const int s0 = cu[b], L = min(cu[b + 1] - s0, lmax);
-    for (int q0 = 0; q0 < L; q0 += kAttnQ) plan[at++] = make_int4(s0, L, q0, min(kAttnQ, L - q0));
+    for (int q0 = 0; q0 < L; q0 += kAttnQ, at++)
+      if (at < max_tiles) plan[at] = make_int4(s0, L, q0, min(kAttnQ, L - q0));
   }
   for (int t = part[0] + tid; t < max_tiles; t += 256) plan[t] = make_int4(0, 0, 0, 0);
 }
