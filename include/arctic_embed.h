@@ -194,6 +194,19 @@ int ae_attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev, int
  * AE_ERR_INVALID_ARG. */
 int ae_attention_varlen_quantized(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
                                   int total_tokens, float* ctx_dev, void* stream);
+/* No counterpart in the reference: ae_attention_varlen for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It allocates nothing, copies nothing to the
+ * host and does not synchronize: the caller states max_seq_len (1..512), every
+ * segment must hold 1..max_seq_len tokens (rows of a longer one are
+ * unspecified).  The only scratch, the tile plan, is a static device array of
+ * 65536 records (1 MiB, held by each GPU the library runs on until the process
+ * ends): total_tokens / 32 + n_seqs + 1 <= 65536, else AE_ERR_CAPACITY.  All
+ * calls on one GPU share that array, so calls that overlap on one GPU race.
+ * The first call on a device (current) resolves the array's address there and
+ * must not be inside a stream capture. */
+int ae_attention_varlen_noalloc(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs,
+                                int total_tokens, int max_seq_len, float* ctx_dev, void* stream);
 /* ae_attention_varlen / ae_attention_varlen_quantized on a workspace's scratch,
  * for callers that run the operator per layer (the reference's per-layer
  * attention call, src/model.rs:607-694): asynchronous on `stream` (NULL: the

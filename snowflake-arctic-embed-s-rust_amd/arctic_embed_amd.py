@@ -69,6 +69,7 @@ _SIGS = {
     "ae_workspace_attention_varlen": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "ae_workspace_attention_varlen_quantized": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "ae_workspace_synchronize": (_i32, [_vp, _vp]),
+    "ae_attention_varlen_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "ae_write_synthetic_ae8": (_i32, [_c.c_char_p, _u64]),
     "ae_tokenizer_open": (_i32, [_c.c_char_p, _c.POINTER(_vp)]),
     "ae_tokenizer_close": (None, [_vp]),
@@ -442,6 +443,12 @@ def gelu_smooth_quantize(m, n, x_ptr, smooth_ptr, q_ptr, scale_ptr, stream=None)
 
 def attention_varlen(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None):
     _check(_lib.ae_attention_varlen(qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), ctx_ptr, stream))
+
+
+def attention_varlen_noalloc(qkv_ptr, cu_ptr, n_seqs, total_tokens, max_seq_len, ctx_ptr, stream=None):
+    """attention_varlen with no allocation, host copy or synchronization (static device scratch)."""
+    _check(_lib.ae_attention_varlen_noalloc(qkv_ptr, cu_ptr, int(n_seqs), int(total_tokens), int(max_seq_len),
+                                            ctx_ptr, stream))
 
 
 def attention_varlen_quantized(qkv_ptr, cu_ptr, n_seqs, total_tokens, ctx_ptr, stream=None):

@@ -2,6 +2,8 @@
 // [CLS]-only attention, both in the reference's exact scalar evaluation order.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -682,6 +684,40 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
     hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
   else
     hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles);
+}
+
+// ---------------------------------------------------------------------------
+// The attention operator's only scratch, the tile plan, in a file-scope device
+// array for callers that cannot allocate (ae_attention_varlen_noalloc).  Each
+// GPU holds its own copy until the process ends; host code reaches it only
+// through the per-device address that hipGetSymbolAddress returns (the array's
+// name is a host-side stand-in, not a device address).  Every call on a GPU
+// shares that GPU's array: calls that overlap on one GPU race.  The plan kernel
+// rewrites every record a launch reads, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) int4 scratch[kNoAllocPlanTiles];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+int* g_noalloc_plan[kNoAllocMaxDevices] = {};
+}  // namespace
+
+hipError_t noalloc_plan_scratch(int** plan) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_plan[dev]) {  // first call on this device (current): resolve its copy once
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    init_attention_kernels();
+    g_noalloc_plan[dev] = static_cast<int*>(ptr);
+  }
+  *plan = g_noalloc_plan[dev];
+  return hipSuccess;
 }
 
 void launch_attention_short(const AttnArgs& p, hipStream_t st) {

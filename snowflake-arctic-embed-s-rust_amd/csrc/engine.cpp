@@ -986,6 +986,29 @@ static int attention_varlen(const float* qkv_dev, const int32_t* cu_seqlens_dev,
   return AE_OK;
 }
 
+// ae_attention_varlen for callers that cannot allocate: the tile plan lives in
+// a static device array (aek::noalloc_plan_scratch), the caller states
+// max_seq_len, and nothing is allocated, copied to the host or synchronized.
+int ae_attention_varlen_noalloc(const float* qkv_dev, const int32_t* cu_seqlens_dev, int n_seqs, int total_tokens,
+                                int max_seq_len, float* ctx_dev, void* stream) {
+  if (!qkv_dev || !cu_seqlens_dev || !ctx_dev || n_seqs < 0 || total_tokens < n_seqs || max_seq_len < 1 ||
+      max_seq_len > ae::kMaxPos)
+    return fail(AE_ERR_INVALID_ARG, "bad attention arguments (max_seq_len must be 1..512)");
+  if (n_seqs == 0) return AE_OK;
+  if (aek::attention_max_tiles(n_seqs, total_tokens) > aek::kNoAllocPlanTiles)
+    return fail(AE_ERR_CAPACITY, "ae_attention_varlen_noalloc: total_tokens / 32 + n_seqs + 1 = " +
+                                     std::to_string(aek::attention_max_tiles(n_seqs, total_tokens)) +
+                                     " exceeds its static scratch of " + std::to_string(aek::kNoAllocPlanTiles) +
+                                     " tiles");
+  int* plan = nullptr;
+  const hipError_t e = aek::noalloc_plan_scratch(&plan);
+  if (e != hipSuccess) return fail(AE_ERR_HIP, std::string("no-allocation attention scratch: ") + hipGetErrorString(e));
+  aek::AttnArgs a{qkv_dev, cu_seqlens_dev, n_seqs, plan, ctx_dev, nullptr, nullptr, aek::attention_pitch(max_seq_len)};
+  aek::launch_attention(a, total_tokens, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
 // The same operators on the workspace's scratch: no allocation after the first
 // quantized call, no host copy, no synchronization.  The caller bounds the
 // segment lengths (max_seq_len, 1..512); a batch that breaks the bound, or whose

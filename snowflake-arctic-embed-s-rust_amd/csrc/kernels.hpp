@@ -117,6 +117,12 @@ inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
 // ints of `plan` scratch for B segments and T tokens: one 4-int record per tile
 inline size_t attention_plan_ints(int B, int T) { return 4 * (size_t)attention_max_tiles(B, T); }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
+// ae_attention_varlen_noalloc: the tile plan in a static device array of this
+// many records (1 MiB), so attention_max_tiles(B, T) <= kNoAllocPlanTiles
+constexpr int kNoAllocPlanTiles = 65536;
+// the current device's address of that array (resolved on the first call per
+// device, with the device current; not during a stream capture)
+hipError_t noalloc_plan_scratch(int** plan);
 // T = total tokens of the batch; plan = false reuses the plan already in p.plan
 // (launch_attention_plan, which depends only on cu, B, T and s_pitch)
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
