@@ -147,8 +147,6 @@ struct ae_workspace {
   int attention_mode = AE_ATTENTION_EXACT;
   aek::SmeArgs sme{};
   int* err = nullptr;        // device error word: bit 0 = a packed batch with a bad segment (ae_workspace_synchronize)
-  int* splitk = nullptr;     // int32 partial sums of split-K GEMMs (small M)
-  size_t splitk_ints = 0;
   float *hidden = nullptr, *tmp = nullptr, *qkv = nullptr, *ctx = nullptr, *g = nullptr;
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
@@ -337,8 +335,6 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.out = o;
     p.g_smooth = g_smooth;
     p.g_rowmax = g_rowmax;
-    p.partial = ws->splitk;
-    p.partial_ints = ws->splitk_ints;
     return p;
   };
   auto gemm = [&](const ae_linear& L, int M, const void* A, int amode, const float* a_scale, const uint32_t* a_rowmax,
@@ -360,10 +356,10 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.rowmax_init = rowmax_init;
     return p;
   };
-  // an N = 384 GEMM and the LayerNorm of its output: one fused split-K epilogue
-  // when the GEMM splits K (few rows, latency-bound), else the two kernels
+  // an N = 384 GEMM and the LayerNorm of its output: one kernel for few rows
+  // (latency-bound), else the two kernels
   auto gemm_then_ln = [&](int gemm_kind, int ln_kind, const GemmArgs& g, int amode, const LnArgs& l) {
-    if (gemm_splits_k(g)) {
+    if (gemm_fuses_ln(g)) {
       KernelTimer kt(ws, st, gemm_kind);
       launch_gemm_ln(g, amode, l, st);
       return;
@@ -483,12 +479,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
                                  ws->hidden_c, ws->tmp_c, nullptr, nullptr);
     const LnArgs l = ln_args(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c,
                              ws->act_scale_c, ws->rowmax_g_c, B);
-    if (gemm_splits_k(g)) {
-      launch_gemm_ln(g, kAF32QSmooth, l, st);
-    } else {
-      launch_gemm(g, kAF32QSmooth, kEpiF32, st);
-      launch_ln_quant(l, kLnSrcF32, st);
-    }
+    launch_gemm_ln(g, kAF32QSmooth, l, st);
   }
   gemm(D.ffn_inter, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->g_c, kEpiGelu,
        D.ffn_out.inv_smooth, ws->rowmax_g_c);
@@ -716,10 +707,6 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
       (rc = A(&ws->act_q_c, B * 384)) || (rc = A(&ws->act_scale_c, B)) || (rc = A(&ws->rowmax_ctx_c, B)) ||
       (rc = A(&ws->rowmax_g_c, B)))
     return rc;
-  // split-K partials: at most ~4.7 M int32 for any GEMM shape here once the grid
-  // is small enough to split; launch_gemm lowers the split count to fit
-  ws->splitk_ints = std::min<size_t>(size_t(6) << 20, 3 * T * 1536);
-  if ((rc = A(&ws->splitk, ws->splitk_ints))) return rc;
   HIP_TRY(hipMemset(ws->err, 0, sizeof(int)));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_ids), T * sizeof(uint16_t), hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ws->h_cu), (B + 1) * sizeof(int), hipHostMallocDefault));

@@ -65,24 +65,18 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   // back on one XCD and their A rows come from HBM once (f32 A always; int8 A
   // when A is too large to stay in the Infinity Cache between column tiles).
   // Otherwise row tile fastest: neighbouring workgroups share W columns.
-  // Split K (p.ksplit > 1, small M): the grid repeats the items once per K range
-  // and each workgroup writes its raw int32 sums to p.partial[split][M][N];
-  // gemm_splitk_epilogue_kernel adds them (exact: integers) and applies the
-  // epilogue below.
-  const int nt = p.N / kBN, mt = (p.M + kBM - 1) / kBM;
-  const int ks = p.ksplit > 1 ? p.ksplit : 1, nbase = mt * nt;
-  const int split = blockIdx.x / nbase, bid = blockIdx.x - split * nbase;
+  const int nt = p.N / kBN, mt = (p.M + kBM - 1) / kBM, nbase = mt * nt;
+  const int bid = blockIdx.x;
   int m0, n0;
   if (!p.col_fast) {
     m0 = (bid % mt) * kBM;
     n0 = (bid / mt) * kBN;
   } else {
-    const int item = ks == 1 ? xcd_contiguous(bid, nbase) : bid;
+    const int item = xcd_contiguous(bid, nbase);
     m0 = (item / nt) * kBM;
     n0 = (item % nt) * kBN;
   }
-  const int KB = split * (p.K >> 6) / ks;            // first K step of this workgroup
-  const int KT = (split + 1) * (p.K >> 6) / ks - KB;  // K steps of this workgroup
+  const int KB = 0, KT = p.K >> 6;  // K steps
   const int NB = p.N >> 4;  // 16-column fragments per K step in the swizzled W
   const ExpTab tb = exp_tab_regs();  // the epilogue loop below is wave-uniform
 
@@ -183,27 +177,6 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   // accumulators -> sE[16][96] (int32), then lanes walk rows with float4s
   int* E = sE[wave];
   const int col0 = n0 + wave * kWaveN;  // first column of this wave
-  if (ks > 1) {  // raw sums of this K range (uniform branch)
-    int* part = p.partial + (size_t)split * p.M * p.N;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int j = 0; j < kCB; j++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
-      wave_lds_sync();
-#pragma unroll
-      for (int k = 0; k < kF4 / 4; k++) {
-        const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
-        const int row = m0 + i * 16 + rr;
-        if (row < p.M)
-          *reinterpret_cast<int4*>(part + (size_t)row * p.N + col0 + c4 * 4) =
-              *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
-      }
-      wave_lds_sync();
-    }
-    return;
-  }
   // Epilogue operands.  The row scales and the w_scale / bias columns of this
   // workgroup, loaded at the start (ep_reg), are in LDS (sEp*) by now.  Lane
   // (k, idx = lane + 64k) covers block row idx / kF4 and float4 column idx % kF4
@@ -281,175 +254,292 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
   }
 }
 
-// Split-K epilogue: out[row][col..col+3] from the int32 sums of the p.ksplit K
-// ranges, with the same arithmetic as gemm_w8a8_kernel's epilogue.  Block
-// (x, row) covers 256 float4 columns of one row; every lane evaluates (the
-// exact GELU needs the whole wave) and only in-range lanes write.  The GELU row
-// absmax is the max over u32 bits of the same per-float4 values the fused
-// epilogue feeds to atomicMax.
-template <int AM, int EM>
-__global__ __launch_bounds__(256) void gemm_splitk_epilogue_kernel(GemmArgs p) {
-  const ExpTab tb = exp_tab_regs();
-  const int row = blockIdx.y, n4 = p.N >> 2;
-  const int c4 = blockIdx.x * 256 + threadIdx.x;
-  const bool in = c4 < n4;
-  const int col = 4 * min(c4, n4 - 1);
-  int4 a4 = make_int4(0, 0, 0, 0);
-  for (int sp = 0; sp < p.ksplit; sp++) {
-    const int4 v = *reinterpret_cast<const int4*>(p.partial + ((size_t)sp * p.M + row) * p.N + col);
-    a4.x += v.x; a4.y += v.y; a4.z += v.z; a4.w += v.w;
-  }
-  float sa;
-  if (AM == kAI8) sa = p.a_scale[row];
-  else sa = __uint_as_float(p.a_rowmax[row]) / 127.0f;  // scale = max_abs / 127.0
-  const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
-  float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
-  if (p.res) {
-    const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)row * p.N + col);
-    b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
-  }
-  float4 v;
-  v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
-  v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
-  v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
-  v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
-  if (EM == kEpiGelu) {
-    const float4 g4 = *reinterpret_cast<const float4*>(p.g_smooth + col);
-    v.x = gelu_exact(v.x, tb) * g4.x;
-    v.y = gelu_exact(v.y, tb) * g4.y;
-    v.z = gelu_exact(v.z, tb) * g4.z;
-    v.w = gelu_exact(v.w, tb) * g4.w;
-    const float gm = nanless_max(nanless_max(fabsf(v.x), fabsf(v.y)), nanless_max(fabsf(v.z), fabsf(v.w)));
-    uint32_t gb = in ? __float_as_uint(gm) : 0u;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) gb = max(gb, (uint32_t)__shfl_xor((int)gb, off, 64));
-    if ((threadIdx.x & 63) == 0 && gb != 0u) atomicMax(&p.g_rowmax[row], gb);
-  }
-  if (in) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
-}
+// ---------------------------------------------------------------------------
+// Small M (latency-bound launches: single sequences, short batches, the
+// layer-11 tail): 16 rows per workgroup, four times the workgroups of the
+// 64-row tiles.  The workgroup stages its whole A tile (16 x K int8; f32 A is
+// quantized on the way, as astore does above) into LDS once, so the K loop has
+// no barrier; each wave streams its B fragments through a register ring
+// kRing K steps deep, which hides the L2 latency of those loads.  The residual
+// rows are loaded before the K loop.  Each wave owns 48 columns; with 8 waves
+// the workgroup spans all 384 columns, and with LN it applies the LayerNorm +
+// SmoothQuant of `ln` to its 16 output rows (layernorm_smooth_quantize_row_scalar,
+// reference src/simd_math.rs:208-247; p.out is then not written).
+// ---------------------------------------------------------------------------
+constexpr int kSmallMaxK = 1536;
+constexpr int kSmallPitch = kSmallMaxK + 16;  // LDS bytes per A row: conflict-free fragment reads
+constexpr int kLnPitchS = 388;                // LDS floats per row of the fused LayerNorm
 
-// Split-K epilogue of an N = 384 GEMM (kEpiF32) with the LayerNorm +
-// SmoothQuant of each output row fused: ln_quant_kernel's arithmetic in the
-// same order (layernorm_smooth_quantize_row_scalar, reference
-// src/simd_math.rs:208-247), one 128-thread block per row.  The GEMM output row
-// stays in LDS; only the LayerNorm results (ln.dst, ln.q, ln.scale) are stored.
-// ln.dst may equal p.res: each block reads its residual row before the barrier
-// that precedes its stores.
-template <int AM>
-__global__ __launch_bounds__(128) void gemm_splitk_epilogue_ln_kernel(GemmArgs p, LnArgs ln) {
-  __shared__ __attribute__((aligned(16))) float xrow[384];
-  __shared__ float s_stat[2], s_amax[2];
-  const int row = blockIdx.x, t = threadIdx.x;
-  const bool own = t < 96;  // float4 column 4t of the row
-  const int col = 4 * min(t, 95);
-  if (own) {
-    int4 a4 = make_int4(0, 0, 0, 0);
-    for (int sp = 0; sp < p.ksplit; sp++) {
-      const int4 v = *reinterpret_cast<const int4*>(p.partial + ((size_t)sp * p.M + row) * 384 + col);
-      a4.x += v.x; a4.y += v.y; a4.z += v.z; a4.w += v.w;
+template <int AM, int EM, int WAVES, bool LN>
+__global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnArgs ln) {
+  constexpr int NW = 48, kThreads = 64 * WAVES;
+  constexpr int kBN = WAVES * NW, kCB = NW / 16, kF4 = NW / 4, kEk = kF4 / 4;
+  constexpr int kRing = 8;
+  static_assert(!LN || (WAVES == 8 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
+  __shared__ __attribute__((aligned(16))) int8_t sA[16 * kSmallPitch];
+  __shared__ __attribute__((aligned(16))) int sE[WAVES][16 * kEPitch];
+  static_assert(!LN || sizeof(sE) >= 16 * kLnPitchS * sizeof(float), "LN squares reuse the staging tile");
+  __shared__ uint32_t sRowMax[WAVES][16];
+  __shared__ __attribute__((aligned(16))) float sEpSa[16], sEpWs[kBN], sEpB[kBN];
+  __shared__ __attribute__((aligned(16))) float sLn[LN ? 16 * kLnPitchS : 4];
+  __shared__ float s_stat[2][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fk = (lane >> 4) * 16;
+  const int mt = (p.M + 15) >> 4;
+  const int m0 = (blockIdx.x % mt) * 16, n0 = (blockIdx.x / mt) * kBN;
+  const int KT = p.K >> 6, NB = p.N >> 4;
+  const int col0 = n0 + wave * NW;
+  const ExpTab tb = exp_tab_regs();  // the epilogue below is wave-uniform
+
+  // B ring: the first kRing K steps, issued first
+  const int cb0 = col0 >> 4;
+  const int8_t* wbase = p.w + (size_t)lane * 16;
+  v4i bring[kRing][kCB];
+  auto bload = [&](int kt, v4i (&dst)[kCB]) {
+#pragma unroll
+    for (int j = 0; j < kCB; j++) dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + cb0 + j) * 1024);
+  };
+#pragma unroll
+  for (int u = 0; u < kRing; u++)
+    if (u < KT) bload(u, bring[u]);
+  // epilogue operands: row scales, w_scale and bias of the workgroup's columns
+  float4 ep_reg = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (tid < 16) {
+    const int r = min(m0 + tid, p.M - 1);
+    ep_reg.x = AM == kAI8 ? p.a_scale[r] : __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
+  } else if (tid < 16 + kBN / 4) {
+    ep_reg = reinterpret_cast<const float4*>(p.w_scale + n0)[tid - 16];
+  } else if (tid < 16 + kBN / 2) {
+    ep_reg = reinterpret_cast<const float4*>(p.bias + n0)[tid - 16 - kBN / 4];
+  }
+  // residual float4s of this lane's epilogue positions
+  float4 resv[kEk];
+  if (p.res) {
+#pragma unroll
+    for (int k = 0; k < kEk; k++) {
+      const int idx = lane + 64 * k;
+      const int row = min(m0 + idx / kF4, p.M - 1);
+      resv[k] = *reinterpret_cast<const float4*>(p.res + (size_t)row * p.N + col0 + (idx % kF4) * 4);
     }
-    float sa;
-    if (AM == kAI8) sa = p.a_scale[row];
-    else sa = __uint_as_float(p.a_rowmax[row]) / 127.0f;  // scale = max_abs / 127.0
-    const float4 ws4 = *reinterpret_cast<const float4*>(p.w_scale + col);
-    float4 b4 = *reinterpret_cast<const float4*>(p.bias + col);
+  }
+  // the A tile: 16 rows x K as 16-byte chunks (16 k-values); thread t takes
+  // chunks t + kThreads * i.  Every load is issued before any is used (one
+  // round trip), then f32 A is quantized as astore does above.
+  {
+    constexpr int kChunks = 16 * kSmallMaxK / 16 / kThreads;  // per thread at the largest K
+    const int cpr = p.K >> 4, nch = 16 * cpr;            // chunks per row, in the tile
+    if constexpr (AM == kAI8) {
+      v4i q[kChunks];
+#pragma unroll
+      for (int i = 0; i < kChunks; i++) {
+        const int c = tid + kThreads * i, r = c / cpr;
+        if (c < nch)
+          q[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(p.A) +
+                                               (size_t)min(m0 + r, p.M - 1) * p.K + (c - r * cpr) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < kChunks; i++) {
+        const int c = tid + kThreads * i, r = c / cpr;
+        if (c < nch) *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + (c - r * cpr) * 16]) = q[i];
+      }
+    } else {
+      float4 x[kChunks][4];
+      float a_inv[kChunks];
+#pragma unroll
+      for (int i = 0; i < kChunks; i++) {
+        const int c = tid + kThreads * i, r = c / cpr;
+        if (c < nch) {
+          const int row = min(m0 + r, p.M - 1);
+          const float4* src =
+              reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.A) + (size_t)row * p.K + (c - r * cpr) * 16);
+#pragma unroll
+          for (int k = 0; k < 4; k++) x[i][k] = src[k];
+          a_inv[i] = __uint_as_float(p.a_rowmax[row]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kChunks; i++) {
+        const int c = tid + kThreads * i, r = c / cpr, kc = (c - r * cpr) * 16;
+        if (c < nch) {
+          const float inv = 127.0f / a_inv[i];  // inv_scale = 127.0 / max_abs
+          uint32_t w[4];
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            float4 v = x[i][k];
+            if (AM == kAF32QSmooth) {  // (x * inv_smooth[j]) * inv_scale
+              const float4 sm = reinterpret_cast<const float4*>(p.a_smooth + kc)[k];
+              v.x = v.x * sm.x; v.y = v.y * sm.y; v.z = v.z * sm.z; v.w = v.w * sm.w;
+            }
+            w[k] = pack4(qround(v.x * inv), qround(v.y * inv), qround(v.z * inv), qround(v.w * inv));
+          }
+          *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + kc]) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        }
+      }
+    }
+  }
+  if (tid < 16) sEpSa[tid] = ep_reg.x;
+  else if (tid < 16 + kBN / 4) reinterpret_cast<float4*>(sEpWs)[tid - 16] = ep_reg;
+  else if (tid < 16 + kBN / 2) reinterpret_cast<float4*>(sEpB)[tid - 16 - kBN / 4] = ep_reg;
+  __syncthreads();
+
+  v4i acc[kCB];
+#pragma unroll
+  for (int j = 0; j < kCB; j++) acc[j] = v4i{0, 0, 0, 0};
+  for (int k0 = 0; k0 < KT; k0 += kRing) {
+#pragma unroll
+    for (int u = 0; u < kRing; u++) {
+      const int kt = k0 + u;
+      if (kt < KT) {  // wave-uniform
+        const v4i af = *reinterpret_cast<const v4i*>(&sA[fr * kSmallPitch + kt * 64 + fk]);
+#pragma unroll
+        for (int j = 0; j < kCB; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bring[u][j], acc[j], 0, 0, 0);
+        if (kt + kRing < KT) bload(kt + kRing, bring[u]);
+      }
+    }
+  }
+
+  // epilogue: the accumulators through this wave's LDS tile, then whole rows
+  int* E = sE[wave];
+#pragma unroll
+  for (int j = 0; j < kCB; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[j][r];
+  if (EM == kEpiGelu && lane < 16) sRowMax[wave][lane] = 0u;
+  wave_lds_sync();  // E and sRowMax are private to this wave
+#pragma unroll
+  for (int k = 0; k < kEk; k++) {  // 16 rows x kF4 float4 over 64 lanes
+    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
+    const int row = m0 + rr, col = col0 + c4 * 4;
+    const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
+    const float sa = sEpSa[rr];
+    const float4 ws4 = *reinterpret_cast<const float4*>(&sEpWs[wave * NW + c4 * 4]);
+    float4 b4 = *reinterpret_cast<const float4*>(&sEpB[wave * NW + c4 * 4]);
     if (p.res) {
-      const float4 r4 = *reinterpret_cast<const float4*>(p.res + (size_t)row * 384 + col);
-      b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+      b4.x = b4.x + resv[k].x; b4.y = b4.y + resv[k].y; b4.z = b4.z + resv[k].z; b4.w = b4.w + resv[k].w;
     }
     float4 v;
     v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
     v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
     v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
     v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
-    *reinterpret_cast<float4*>(&xrow[col]) = v;
+    if (EM == kEpiGelu) {
+      const float4 g4 = *reinterpret_cast<const float4*>(p.g_smooth + col);
+      v.x = gelu_exact(v.x, tb) * g4.x;
+      v.y = gelu_exact(v.y, tb) * g4.y;
+      v.z = gelu_exact(v.z, tb) * g4.z;
+      v.w = gelu_exact(v.w, tb) * g4.w;
+      float gm = nanless_max(nanless_max(fabsf(v.x), fabsf(v.y)), nanless_max(fabsf(v.z), fabsf(v.w)));
+      atomicMax(&sRowMax[wave][rr], __float_as_uint(gm));  // non-negative f32 bits order like u32
+    }
+    if constexpr (LN) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + col]) = v;
+    else if (row < p.M) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
   }
-  __syncthreads();
-  if (t == 0) {  // sequential sums over the row, in index order
-    const float mean = lds_row_sum(xrow, [](float x) { return x; }) / 384.0f;
-    const float var_sum = lds_row_sum(xrow, [mean](float x) {
-      const float d = x - mean;
-      return d * d;
-    });
-    s_stat[0] = mean;
-    s_stat[1] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
-  }
-  __syncthreads();
-  const float mean = s_stat[0], rstd = s_stat[1];
-  const float4 x = *reinterpret_cast<const float4*>(&xrow[col]);
-  const float4 g = *reinterpret_cast<const float4*>(ln.gamma + col);
-  const float4 b = *reinterpret_cast<const float4*>(ln.beta + col);
-  const float4 sm = *reinterpret_cast<const float4*>(ln.smooth + col);
-  float4 y;
-  y.x = (x.x - mean) * rstd * g.x + b.x;
-  y.y = (x.y - mean) * rstd * g.y + b.y;
-  y.z = (x.z - mean) * rstd * g.z + b.z;
-  y.w = (x.w - mean) * rstd * g.w + b.w;
-  if (own) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + col) = y;
-  const float4 ys = make_float4(y.x * sm.x, y.y * sm.y, y.z * sm.z, y.w * sm.w);
-  float amax = 0.0f;
-  if (own) {
-    amax = nanless_max(amax, fabsf(ys.x));
-    amax = nanless_max(amax, fabsf(ys.y));
-    amax = nanless_max(amax, fabsf(ys.z));
-    amax = nanless_max(amax, fabsf(ys.w));
-  }
+  wave_lds_sync();
+  if (EM == kEpiGelu && lane < 16 && m0 + lane < p.M) atomicMax(&p.g_rowmax[m0 + lane], sRowMax[wave][lane]);
+  if constexpr (LN) {
+    // sequential sums per row (one lane each), then 32 lanes per row normalize
+    // and quantize; ln.dst may equal p.res (its rows were loaded above)
+    const int rr = tid >> 5, sub = tid & 31, row = m0 + rr;
+    float4 g[3], b[3], sm[3];
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
-  if ((t & 63) == 0) s_amax[t >> 6] = amax;
-  __syncthreads();
-  const float max_abs = nanless_max(1e-8f, nanless_max(s_amax[0], s_amax[1]));
-  const float inv_scale = 127.0f / max_abs;
-  if (own)
-    *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + col) =
-        pack4(qround(ys.x * inv_scale), qround(ys.y * inv_scale), qround(ys.z * inv_scale), qround(ys.w * inv_scale));
-  if (t == 0) {
-    ln.scale[row] = max_abs / 127.0f;
-    if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
-    if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      g[i] = *reinterpret_cast<const float4*>(ln.gamma + c);
+      b[i] = *reinterpret_cast<const float4*>(ln.beta + c);
+      sm[i] = *reinterpret_cast<const float4*>(ln.smooth + c);
+    }
+    // The in-order sums are the only serial part: one lane per row adds, every
+    // other step (the squares (x - mean)^2 included) runs on all 512 threads.
+    // A lone wave issues about one VALU instruction per 5 cycles, so a chain that
+    // also formed the squares would take three instructions per element.
+    __syncthreads();
+    if (tid < 16) s_stat[0][tid] = lds_row_sum(&sLn[tid * kLnPitchS], [](float x) { return x; }) / 384.0f;
+    __syncthreads();
+    const float mean = s_stat[0][rr];
+    float* sSq = reinterpret_cast<float*>(&sE[0][0]);  // the epilogue staging is free now: (x - mean)^2 rows
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      float4 d = *reinterpret_cast<const float4*>(&sLn[rr * kLnPitchS + c]);
+      d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+      *reinterpret_cast<float4*>(&sSq[rr * kLnPitchS + c]) = make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
+    }
+    __syncthreads();
+    if (tid < 16) {
+      const float var_sum = lds_row_sum(&sSq[tid * kLnPitchS], [](float x) { return x; });
+      s_stat[1][tid] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
+    }
+    __syncthreads();
+    const float rstd = s_stat[1][rr];
+    float4 ys[3];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      const float4 x = *reinterpret_cast<const float4*>(&sLn[rr * kLnPitchS + c]);
+      float4 y;
+      y.x = (x.x - mean) * rstd * g[i].x + b[i].x;
+      y.y = (x.y - mean) * rstd * g[i].y + b[i].y;
+      y.z = (x.z - mean) * rstd * g[i].z + b[i].z;
+      y.w = (x.w - mean) * rstd * g[i].w + b[i].w;
+      if (row < p.M) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + c) = y;
+      ys[i] = make_float4(y.x * sm[i].x, y.y * sm[i].y, y.z * sm[i].z, y.w * sm[i].w);
+      amax = nanless_max(amax, fabsf(ys[i].x));
+      amax = nanless_max(amax, fabsf(ys[i].y));
+      amax = nanless_max(amax, fabsf(ys[i].z));
+      amax = nanless_max(amax, fabsf(ys[i].w));
+    }
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+    const float max_abs = nanless_max(1e-8f, amax);
+    const float inv_scale = 127.0f / max_abs;
+    if (row < p.M) {
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const int c = (sub + 32 * i) * 4;
+        *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + c) =
+            pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale), qround(ys[i].z * inv_scale),
+                  qround(ys[i].w * inv_scale));
+      }
+      if (sub == 0) {
+        ln.scale[row] = max_abs / 127.0f;
+        if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
+        if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
+      }
+    }
   }
 }
 
-// Workgroups of 64 rows x 192 columns.  Small M (fewer than kSplitGrid
-// workgroups) splits K into ranges of at least two steps when the caller
-// provides int32 scratch (GemmArgs::partial) for the partial sums.
-constexpr int kSplitGrid = 192;
+// Up to this many rows (and K <= kSmallMaxK) the GEMMs take gemm_small_kernel.
+constexpr int kSmallM = 1024;
 // int8 A of more bytes than this is re-read from HBM if each column tile walks
 // all row tiles (measured: 113 MB of A at M = 294,912 runs 8-12 % faster column
 // tile fastest, 25 MB at M = 65,536 up to 13 % slower)
 constexpr size_t kColFastABytes = size_t(96) << 20;
 
-static int split_k(const GemmArgs& p) {
-  const int mt = (p.M + kBM - 1) / kBM, nbase = mt * (p.N / 192), kt = p.K / 64;
-  int ks = 1;
-  if (p.partial && nbase < kSplitGrid) {
-    ks = std::min((kSplitGrid + nbase - 1) / nbase, kt / 2);
-    ks = (int)std::min<size_t>((size_t)ks, p.partial_ints / ((size_t)p.M * p.N));
-    if (ks < 2) ks = 1;
-  }
-  return ks;
-}
+static bool small_gemm(const GemmArgs& p) { return p.M <= kSmallM && p.K <= kSmallMaxK; }
 
-// ln != null (N = 384, kEpiF32, split K): the epilogue also applies *ln to each
+// ln != null: N = 384, kEpiF32, small_gemm(p); the epilogue applies *ln to each
 // output row and p.out is not written
 template <int AM, int EM>
 static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullptr) {
-  const int nbase = ((p.M + kBM - 1) / kBM) * (p.N / 192);
-  p.ksplit = split_k(p);
-  p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;
-  hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase * p.ksplit), dim3(256), 0, st, p);
-  if (p.ksplit > 1) {
-    if (ln) hipLaunchKernelGGL((gemm_splitk_epilogue_ln_kernel<AM>), dim3(p.M), dim3(128), 0, st, p, *ln);
-    else hipLaunchKernelGGL((gemm_splitk_epilogue_kernel<AM, EM>), dim3((p.N / 4 + 255) / 256, p.M), dim3(256), 0,
-                            st, p);
+  const int mt16 = (p.M + 15) / 16;
+  if (small_gemm(p)) {
+    if (ln) hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, 8, true>), dim3(mt16), dim3(512), 0, st, p, *ln);
+    else hipLaunchKernelGGL((gemm_small_kernel<AM, EM, 4, false>), dim3(mt16 * (p.N / 192)), dim3(256), 0, st, p,
+                            LnArgs{});
+    return;
   }
+  p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;
+  const int nbase = ((p.M + 63) / 64) * (p.N / 192);
+  hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase), dim3(256), 0, st, p);
 }
 
-bool gemm_splits_k(const GemmArgs& p) { return p.M > 0 && split_k(p) > 1; }
+bool gemm_fuses_ln(const GemmArgs& p) { return p.M > 0 && p.N == 384 && small_gemm(p); }
 
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {
   if (p.M <= 0) return;
-  if (p.N != 384 || split_k(p) < 2) {  // no split: the GEMM, then the LayerNorm kernel over its output
+  if (!gemm_fuses_ln(p)) {  // the GEMM, then the LayerNorm kernel over its output
     launch_gemm(p, amode, kEpiF32, st);
     LnArgs l = ln;
     l.src = p.out;

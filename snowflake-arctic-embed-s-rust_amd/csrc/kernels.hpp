@@ -28,9 +28,6 @@ struct GemmArgs {
   float* out;                 // [M,N]
   const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
   uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
-  int* partial;               // optional int32 scratch for split-K partial sums (small M), or null
-  size_t partial_ints;        // its capacity in int32
-  int ksplit;                 // set by launch_gemm
   int col_fast;               // set by launch_gemm: workgroup order (column tile fastest)
 };
 // N % 384 == 0, K % 64 == 0
@@ -89,12 +86,11 @@ void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st);
 // bit 0 of *err when cu[0..B] is not a prefix sum of T with segments of 1..max_len tokens
 void launch_check_segments(const int* cu, int B, int T, int max_len, int* err, hipStream_t st);
 // An N = 384 GEMM (kEpiF32) followed by the LayerNorm + SmoothQuant of its
-// output rows (ln.src is ignored: the GEMM output).  With split K the LayerNorm
-// runs in the split-K epilogue and p.out is not written; otherwise the GEMM
-// writes p.out and launch_ln_quant reads it.
+// output rows (ln.src is ignored: the GEMM output).  When gemm_fuses_ln(p) (few
+// rows) the LayerNorm runs in the GEMM's epilogue and p.out is not written;
+// otherwise the GEMM writes p.out and launch_ln_quant reads it.
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st);
-// whether launch_gemm splits K for these arguments (few rows and split-K scratch given)
-bool gemm_splits_k(const GemmArgs& p);
+bool gemm_fuses_ln(const GemmArgs& p);
 
 void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, float* scale, bool gelu,
                       hipStream_t st);

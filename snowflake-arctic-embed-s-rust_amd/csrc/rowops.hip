@@ -14,8 +14,9 @@ namespace aek {
 //
 // WG = 256 threads, 32 rows.  Phase A stages x into LDS; phase B gives each
 // row to one lane, which forms the mean and variance with the reference's
-// sequential left-to-right sums; phase C normalizes, takes the order-free row
-// absmax and quantizes with 8 lanes per row.  Source modes: f32 rows, or the
+// sequential left-to-right sums (the squared deviations are formed by all
+// threads); phase C normalizes, takes the order-free row absmax and quantizes
+// with 8 lanes per row.  Source modes: f32 rows, or the
 // embedding gather ((w*ws + p*ps) + type0, src/simd_math.rs:1877-1880).
 // ---------------------------------------------------------------------------
 constexpr int kLnRows = 32;
@@ -91,26 +92,33 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
   for (int i = 0; i < 12; i++) *reinterpret_cast<float4*>(&tile[rl * kLnPitch + (sub + 8 * i) * 4]) = xv[i];
   __syncthreads();
 
+  // Sequential sums over the row, in index order: one lane per row adds, all
+  // threads form the squares (x - mean)^2 in between (written over the tile; x
+  // stays in xv).  A lone wave issues about one VALU instruction per 5 cycles,
+  // so a chain that also formed the squares would take three per element.
+  if (tid < kLnRows) s_mean[tid] = lds_row_sum(&tile[tid * kLnPitch], [](float v) { return v; }) / 384.0f;
+  __syncthreads();
+  const float mean = s_mean[rl];
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    float4 d = xv[i];
+    d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+    *reinterpret_cast<float4*>(&tile[rl * kLnPitch + (sub + 8 * i) * 4]) =
+        make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
+  }
+  __syncthreads();
   if (tid < kLnRows) {
-    // sequential sums over the row, in index order
-    const float* xr = &tile[tid * kLnPitch];
-    const float mean = lds_row_sum(xr, [](float v) { return v; }) / 384.0f;
-    const float var_sum = lds_row_sum(xr, [mean](float v) {
-      const float d = v - mean;
-      return d * d;
-    });
-    s_mean[tid] = mean;
+    const float var_sum = lds_row_sum(&tile[tid * kLnPitch], [](float v) { return v; });
     s_rstd[tid] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
   }
   __syncthreads();
 
-  const float mean = s_mean[rl], rstd = s_rstd[rl];
+  const float rstd = s_rstd[rl];
   float amax = 0.0f;
   float4 ys[12];
 #pragma unroll
   for (int i = 0; i < 12; i++) {
     const int c = (sub + 8 * i) * 4;
-    xv[i] = *reinterpret_cast<const float4*>(&tile[rl * kLnPitch + c]);  // re-read: xv is dead across the sums
     const float4 g = LAT ? pg[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.gamma + c);
     const float4 b = LAT ? pb[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.beta + c);
     const float4 s = LAT ? ps[LAT ? i : 0] : *reinterpret_cast<const float4*>(p.smooth + c);
@@ -217,7 +225,7 @@ void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, fl
 // (layernorm_inplace_row + l2_normalize_inplace, src/simd_math.rs:481-497,
 // :2892-2903): one wave per row.  The row sits in LDS; lane 0 takes the three
 // sequential sums (mean, variance, sum of squares) in index order, all lanes
-// the elementwise steps.
+// the elementwise steps (the squares included).
 __global__ __launch_bounds__(256) void final_ln_l2_kernel(int B, const float* src, const float* gamma,
                                                           const float* beta, float* out) {
   __shared__ __attribute__((aligned(16))) float tile[4][kLnPitch];
@@ -233,17 +241,21 @@ __global__ __launch_bounds__(256) void final_ln_l2_kernel(int B, const float* sr
   reinterpret_cast<float4*>(t)[lane] = xa;
   if (two) reinterpret_cast<float4*>(t)[64 + lane] = xb;
   wave_lds_sync();
-  if (lane == 0) {
-    const float mean = lds_row_sum(t, [](float v) { return v; }) / 384.0f;
-    const float var_sum = lds_row_sum(t, [mean](float v) {
-      const float d = v - mean;
-      return d * d;
-    });
-    s_stat[wave][0] = mean;
-    s_stat[wave][1] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
-  }
+  // lane 0 adds, all lanes form the squares in between (written over the row;
+  // x stays in xa / xb)
+  if (lane == 0) s_stat[wave][0] = lds_row_sum(t, [](float v) { return v; }) / 384.0f;
   wave_lds_sync();
-  const float mean = s_stat[wave][0], rstd = s_stat[wave][1];
+  const float mean = s_stat[wave][0];
+  auto sq_dev = [mean](float4 v) {
+    v.x = v.x - mean; v.y = v.y - mean; v.z = v.z - mean; v.w = v.w - mean;
+    return make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+  };
+  reinterpret_cast<float4*>(t)[lane] = sq_dev(xa);
+  if (two) reinterpret_cast<float4*>(t)[64 + lane] = sq_dev(xb);
+  wave_lds_sync();
+  if (lane == 0) s_stat[wave][1] = 1.0f / sqrtf(lds_row_sum(t, [](float v) { return v; }) / 384.0f + 1e-12f);
+  wave_lds_sync();
+  const float rstd = s_stat[wave][1];
   auto ln4 = [&](float4 v, int c4) {
     const float4 g = reinterpret_cast<const float4*>(gamma)[c4];
     const float4 be = reinterpret_cast<const float4*>(beta)[c4];
@@ -255,10 +267,11 @@ __global__ __launch_bounds__(256) void final_ln_l2_kernel(int B, const float* sr
   };
   xa = ln4(xa, lane);
   if (two) xb = ln4(xb, 64 + lane);
-  reinterpret_cast<float4*>(t)[lane] = xa;
-  if (two) reinterpret_cast<float4*>(t)[64 + lane] = xb;
+  auto sq = [](float4 v) { return make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w); };
+  reinterpret_cast<float4*>(t)[lane] = sq(xa);
+  if (two) reinterpret_cast<float4*>(t)[64 + lane] = sq(xb);
   wave_lds_sync();
-  if (lane == 0) s_stat[wave][0] = lds_row_sum(t, [](float v) { return v * v; });
+  if (lane == 0) s_stat[wave][0] = lds_row_sum(t, [](float v) { return v; });
   wave_lds_sync();
   const float sum_sq = s_stat[wave][0];
   float4* y4 = reinterpret_cast<float4*>(out + (size_t)b * H);
