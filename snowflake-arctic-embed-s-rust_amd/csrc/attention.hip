@@ -741,6 +741,7 @@ __global__ __launch_bounds__(128) void gather_cls_kernel(ClsArgs p) {
   if (t == 0) {
     p.act_scale_c[b] = p.act_scale[src];
     p.rowmax_init[b] = __float_as_uint(1e-8f);
+    if (p.rowmax_init2) p.rowmax_init2[b] = __float_as_uint(1e-8f);
   }
 }
 

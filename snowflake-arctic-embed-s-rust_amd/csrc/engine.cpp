@@ -343,7 +343,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     launch_gemm(gemm_args(L, M, A, a_scale, a_rowmax, a_smooth, res, o, g_smooth, g_rowmax), amode, emode, st);
   };
   auto ln_args = [&](const float* src, float* dst, const float* gw, const float* gb, const float* smooth, int8_t* q,
-                     float* scale, uint32_t* rowmax_init, int rows) {
+                     float* scale, uint32_t* rowmax_init, int rows, uint32_t* rowmax_init2 = nullptr) {
     LnArgs p{};
     p.T = rows;
     p.src = src;
@@ -354,6 +354,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.q = q;
     p.scale = scale;
     p.rowmax_init = rowmax_init;
+    p.rowmax_init2 = rowmax_init2;
     return p;
   };
   // an N = 384 GEMM and the LayerNorm of its output: one kernel for few rows
@@ -390,6 +391,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.q = ws->act_q;
     p.scale = ws->act_scale;
     p.rowmax_init = ws->rowmax_ctx;
+    p.rowmax_init2 = gemm_small_path(T) ? ws->rowmax_g : nullptr;
     p.max_len = max_len;
     p.err = ws->err;
     launch_ln_quant(p, kLnSrcEmb, st);
@@ -403,12 +405,29 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   if (sme && !ws->sme.vt) return fail(AE_ERR_INVALID_ARG, "quantized attention scratch missing");
   SmeArgs sme_args = ws->sme;
   sme_args.per_seq = 1;
+  // Few rows (gemm_small_path): every LayerNorm runs in the prologue of the GEMM
+  // that consumes it (QKV, FFN-up, the layer-11 K/V), whose column-tile-0
+  // workgroups also store its outputs, so the attn_out / FFN-down GEMMs spread
+  // their weight columns over twice the workgroups (no whole-row epilogue).
+  // The row-absmax targets of a layer (attention -> rowmax_ctx, GELU -> rowmax_g)
+  // are reset by the LayerNorm that precedes the layer.
+  const bool small = gemm_small_path(T);
+  const float* ln2_w = nullptr;  // small: the previous layer's LN2, applied by the next QKV prologue
+  const float* ln2_b = nullptr;
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
     const DevLayer& D = E->layers[l];
     {
       KernelTimer kt(ws, st, AE_KERNEL_GEMM_QKV);
-      gemm(D.qkv, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->qkv, kEpiF32, nullptr, nullptr);
+      if (small && ln2_w) {
+        launch_gemm_ln_prologue(gemm_args(D.qkv, T, ws->tmp, nullptr, nullptr, nullptr, nullptr, ws->qkv, nullptr,
+                                          nullptr),
+                                ln_args(ws->tmp, ws->hidden, ln2_w, ln2_b, D.qkv_smooth, nullptr, nullptr,
+                                        ws->rowmax_ctx, T, ws->rowmax_g),
+                                kEpiF32, st);
+      } else {
+        gemm(D.qkv, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->qkv, kEpiF32, nullptr, nullptr);
+      }
     }
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
@@ -419,6 +438,29 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       } else {
         launch_attention(a, T, st, /*plan=*/l == 0);  // the tile plan depends only on cu: built once
       }
+    }
+    if (small) {
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
+        gemm(D.attn_out, T, ws->ctx, kAF32QSmooth, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
+             kEpiF32, nullptr, nullptr);
+      }
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
+        launch_gemm_ln_prologue(gemm_args(D.ffn_inter, T, ws->tmp, nullptr, nullptr, nullptr, nullptr, ws->g,
+                                          D.ffn_out.inv_smooth, ws->rowmax_g),
+                                ln_args(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr,
+                                        nullptr, nullptr, T),
+                                kEpiGelu, st);
+      }
+      {
+        KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
+        gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
+             nullptr);
+      }
+      ln2_w = D.ln2_w;
+      ln2_b = D.ln2_b;
+      continue;
     }
     gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1,
                  gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
@@ -448,6 +490,12 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     }
   }
   if (stop_layers >= 0) {
+    if (small && ln2_w) {  // the state after the last layer run: its LN2, as the next QKV would apply it
+      const int s = std::min(stop_layers, ae::kLayers - 1);
+      launch_ln_quant(ln_args(ws->tmp, ws->hidden, ln2_w, ln2_b, E->layers[s].qkv_smooth, ws->act_q, ws->act_scale,
+                              ws->rowmax_ctx, T),
+                      kLnSrcF32, st);
+    }
     hipError_t err = hipGetLastError();
     return err == hipSuccess ? AE_OK : fail(AE_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(err));
   }
@@ -455,7 +503,15 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   KernelTimer kt(ws, st, AE_KERNEL_LAYER11_TAIL);
   const DevLayer& D = E->layers[ae::kLayers - 1];
   float* kv = ws->qkv;  // [T,768]
-  gemm(D.kv_only, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, kv, kEpiF32, nullptr, nullptr);
+  if (small) {  // layer 10's LN2 in the K/V GEMM's prologue; the [CLS] gather reads its act_q / act_scale
+    launch_gemm_ln_prologue(gemm_args(D.kv_only, T, ws->tmp, nullptr, nullptr, nullptr, nullptr, kv, nullptr, nullptr),
+                            ln_args(ws->tmp, ws->hidden, ln2_w, ln2_b, D.qkv_smooth, ws->act_q, ws->act_scale, nullptr,
+                                    T),
+                            kEpiF32, st);
+  } else {
+    gemm(D.kv_only, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, kv, kEpiF32, nullptr, nullptr);
+  }
+  const bool small_tail = gemm_small_path(B);
   ClsArgs c{};
   c.B = B;
   c.cu = cu;
@@ -466,6 +522,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   c.act_q_c = ws->act_q_c;
   c.act_scale_c = ws->act_scale_c;
   c.rowmax_init = ws->rowmax_ctx_c;
+  c.rowmax_init2 = ws->rowmax_g_c;
   c.q_c = ws->q_c;
   c.kv = kv;
   c.ctx_c = ws->ctx_c;
@@ -474,18 +531,31 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   launch_cls(c, 0, st);
   gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
   launch_cls(c, 1, st);
-  {
-    const GemmArgs g = gemm_args(D.attn_out, B, ws->ctx_c, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth,
-                                 ws->hidden_c, ws->tmp_c, nullptr, nullptr);
-    const LnArgs l = ln_args(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c,
-                             ws->act_scale_c, ws->rowmax_g_c, B);
-    launch_gemm_ln(g, kAF32QSmooth, l, st);
+  if (small_tail) {  // LN1 in the FFN-up prologue (rowmax_g_c reset by the [CLS] gather)
+    gemm(D.attn_out, B, ws->ctx_c, kAF32QSmooth, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth, ws->hidden_c,
+         ws->tmp_c, kEpiF32, nullptr, nullptr);
+    launch_gemm_ln_prologue(gemm_args(D.ffn_inter, B, ws->tmp_c, nullptr, nullptr, nullptr, nullptr, ws->g_c,
+                                      D.ffn_out.inv_smooth, ws->rowmax_g_c),
+                            ln_args(ws->tmp_c, ws->hidden_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr, nullptr,
+                                    nullptr, B),
+                            kEpiGelu, st);
+    gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->hidden_c, ws->tmp_c, kEpiF32, nullptr,
+         nullptr);
+    launch_final_ln_l2(B, ws->tmp_c, D.ln2_w, D.ln2_b, out, st);
+  } else {
+    {
+      const GemmArgs g = gemm_args(D.attn_out, B, ws->ctx_c, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth,
+                                   ws->hidden_c, ws->tmp_c, nullptr, nullptr);
+      const LnArgs l = ln_args(ws->tmp_c, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q_c,
+                               ws->act_scale_c, ws->rowmax_g_c, B);
+      launch_gemm_ln(g, kAF32QSmooth, l, st);
+    }
+    gemm(D.ffn_inter, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->g_c, kEpiGelu,
+         D.ffn_out.inv_smooth, ws->rowmax_g_c);
+    gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->tmp_c, ws->hidden_c, kEpiF32, nullptr,
+         nullptr);
+    launch_final_ln_l2(B, ws->hidden_c, D.ln2_w, D.ln2_b, out, st);
   }
-  gemm(D.ffn_inter, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->g_c, kEpiGelu,
-       D.ffn_out.inv_smooth, ws->rowmax_g_c);
-  gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->tmp_c, ws->hidden_c, kEpiF32, nullptr,
-       nullptr);
-  launch_final_ln_l2(B, ws->hidden_c, D.ln2_w, D.ln2_b, out, st);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(AE_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(err));
   return AE_OK;

@@ -276,12 +276,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
   constexpr int kBN = WAVES * NW, kCB = NW / 16, kF4 = NW / 4, kEk = kF4 / 4;
   constexpr int kRing = 8;
   static_assert(!LN || (WAVES == 8 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
+  static_assert(AM != kALn || (WAVES == 4 && !LN), "LayerNorm prologue: 256 threads, 16 per row");
+  constexpr bool kLnTile = LN || AM == kALn;  // an f32 row tile for a LayerNorm
   __shared__ __attribute__((aligned(16))) int8_t sA[16 * kSmallPitch];
   __shared__ __attribute__((aligned(16))) int sE[WAVES][16 * kEPitch];
-  static_assert(!LN || sizeof(sE) >= 16 * kLnPitchS * sizeof(float), "LN squares reuse the staging tile");
+  static_assert(!kLnTile || sizeof(sE) >= 16 * kLnPitchS * sizeof(float), "LN squares reuse the staging tile");
   __shared__ uint32_t sRowMax[WAVES][16];
   __shared__ __attribute__((aligned(16))) float sEpSa[16], sEpWs[kBN], sEpB[kBN];
-  __shared__ __attribute__((aligned(16))) float sLn[LN ? 16 * kLnPitchS : 4];
+  __shared__ __attribute__((aligned(16))) float sLn[kLnTile ? 16 * kLnPitchS : 4];
   __shared__ float s_stat[2][16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fk = (lane >> 4) * 16;
@@ -306,7 +308,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
   float4 ep_reg = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (tid < 16) {
     const int r = min(m0 + tid, p.M - 1);
-    ep_reg.x = AM == kAI8 ? p.a_scale[r] : __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
+    if (AM == kAI8) ep_reg.x = p.a_scale[r];
+    else if (AM != kALn) ep_reg.x = __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
   } else if (tid < 16 + kBN / 4) {
     ep_reg = reinterpret_cast<const float4*>(p.w_scale + n0)[tid - 16];
   } else if (tid < 16 + kBN / 2) {
@@ -328,7 +331,80 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
   {
     constexpr int kChunks = 16 * kSmallMaxK / 16 / kThreads;  // per thread at the largest K
     const int cpr = p.K >> 4, nch = 16 * cpr;            // chunks per row, in the tile
-    if constexpr (AM == kAI8) {
+    if constexpr (AM == kALn) {
+      // LayerNorm + SmoothQuant of the 16 rows (layernorm_smooth_quantize_row_scalar,
+      // reference src/simd_math.rs:208-247, as ln_quant_kernel computes it): one
+      // lane per row takes the in-order sums, 16 threads per row the rest; the
+      // int8 result is the A tile and its scale the epilogue's row scale.
+      const int rr = tid >> 4, sub = tid & 15, row = m0 + rr;
+      const bool writer = n0 == 0 && row < p.M;
+      const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)min(row, p.M - 1) * 384;
+      float4 xv[6], g[6], b[6], sm[6];
+#pragma unroll
+      for (int i = 0; i < 6; i++) {
+        const int c = (sub + 16 * i) * 4;
+        xv[i] = *reinterpret_cast<const float4*>(xr + c);
+        g[i] = *reinterpret_cast<const float4*>(ln.gamma + c);
+        b[i] = *reinterpret_cast<const float4*>(ln.beta + c);
+        sm[i] = *reinterpret_cast<const float4*>(ln.smooth + c);
+      }
+#pragma unroll
+      for (int i = 0; i < 6; i++) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + (sub + 16 * i) * 4]) = xv[i];
+      __syncthreads();
+      if (tid < 16) s_stat[0][tid] = lds_row_sum(&sLn[tid * kLnPitchS], [](float x) { return x; }) / 384.0f;
+      __syncthreads();
+      const float mean = s_stat[0][rr];
+      float* sSq = reinterpret_cast<float*>(&sE[0][0]);  // (x - mean)^2 rows; the staging tile is free until the epilogue
+#pragma unroll
+      for (int i = 0; i < 6; i++) {
+        float4 d = xv[i];
+        d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+        *reinterpret_cast<float4*>(&sSq[rr * kLnPitchS + (sub + 16 * i) * 4]) =
+            make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
+      }
+      __syncthreads();
+      if (tid < 16)
+        s_stat[1][tid] = 1.0f / sqrtf(lds_row_sum(&sSq[tid * kLnPitchS], [](float x) { return x; }) / 384.0f + 1e-12f);
+      __syncthreads();
+      const float rstd = s_stat[1][rr];
+      float4 ys[6];
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 6; i++) {
+        const int c = (sub + 16 * i) * 4;
+        float4 y;
+        y.x = (xv[i].x - mean) * rstd * g[i].x + b[i].x;
+        y.y = (xv[i].y - mean) * rstd * g[i].y + b[i].y;
+        y.z = (xv[i].z - mean) * rstd * g[i].z + b[i].z;
+        y.w = (xv[i].w - mean) * rstd * g[i].w + b[i].w;
+        if (writer) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + c) = y;
+        ys[i] = make_float4(y.x * sm[i].x, y.y * sm[i].y, y.z * sm[i].z, y.w * sm[i].w);
+        amax = nanless_max(amax, fabsf(ys[i].x));
+        amax = nanless_max(amax, fabsf(ys[i].y));
+        amax = nanless_max(amax, fabsf(ys[i].z));
+        amax = nanless_max(amax, fabsf(ys[i].w));
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+      const float max_abs = nanless_max(1e-8f, amax);
+      const float inv_scale = 127.0f / max_abs;
+#pragma unroll
+      for (int i = 0; i < 6; i++) {
+        const int c = (sub + 16 * i) * 4;
+        const uint32_t q4 = pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale),
+                                  qround(ys[i].z * inv_scale), qround(ys[i].w * inv_scale));
+        *reinterpret_cast<uint32_t*>(&sA[rr * kSmallPitch + c]) = q4;
+        if (writer && ln.q) *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + c) = q4;
+      }
+      if (sub == 0) {
+        sEpSa[rr] = max_abs / 127.0f;
+        if (writer) {
+          if (ln.scale) ln.scale[row] = max_abs / 127.0f;
+          if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
+          if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
+        }
+      }
+    } else if constexpr (AM == kAI8) {
       v4i q[kChunks];
 #pragma unroll
       for (int i = 0; i < kChunks; i++) {
@@ -377,9 +453,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
       }
     }
   }
-  if (tid < 16) sEpSa[tid] = ep_reg.x;
-  else if (tid < 16 + kBN / 4) reinterpret_cast<float4*>(sEpWs)[tid - 16] = ep_reg;
-  else if (tid < 16 + kBN / 2) reinterpret_cast<float4*>(sEpB)[tid - 16 - kBN / 4] = ep_reg;
+  if (tid < 16) {
+    if (AM != kALn) sEpSa[tid] = ep_reg.x;
+  } else if (tid < 16 + kBN / 4) {
+    reinterpret_cast<float4*>(sEpWs)[tid - 16] = ep_reg;
+  } else if (tid < 16 + kBN / 2) {
+    reinterpret_cast<float4*>(sEpB)[tid - 16 - kBN / 4] = ep_reg;
+  }
   __syncthreads();
 
   v4i acc[kCB];
@@ -536,6 +616,15 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
 }
 
 bool gemm_fuses_ln(const GemmArgs& p) { return p.M > 0 && p.N == 384 && small_gemm(p); }
+
+bool gemm_small_path(int m) { return m > 0 && m <= kSmallM; }
+
+void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st) {
+  if (p.M <= 0 || p.M > kSmallM || p.K != 384) return;
+  const dim3 grid(((p.M + 15) / 16) * (p.N / 192));
+  if (emode == kEpiGelu) hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, 4, false>), grid, dim3(256), 0, st, p, ln);
+  else hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, 4, false>), grid, dim3(256), 0, st, p, ln);
+}
 
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {
   if (p.M <= 0) return;

@@ -11,6 +11,8 @@ namespace aek {
 constexpr int kAI8 = 0;          // int8 rows + per-row scale
 constexpr int kAF32Q = 1;        // f32 rows quantized on load: q = round(x * (127/max))
 constexpr int kAF32QSmooth = 2;  // f32 rows quantized on load: q = round((x * s_k) * (127/max))
+constexpr int kALn = 3;          // f32 rows (K = 384) put through the LayerNorm + SmoothQuant of an LnArgs
+                                 // first (launch_gemm_ln_prologue, few rows only)
 // GEMM epilogues
 constexpr int kEpiF32 = 0;   // out = fma(f32(acc), sa*ws, bias (+res))
 constexpr int kEpiGelu = 1;  // out = GELU(that) * g_smooth[n]; g_rowmax[m] = max |out|
@@ -91,6 +93,14 @@ void launch_check_segments(const int* cu, int B, int T, int max_len, int* err, h
 // otherwise the GEMM writes p.out and launch_ln_quant reads it.
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st);
 bool gemm_fuses_ln(const GemmArgs& p);
+// Few rows (gemm_small_path): a GEMM whose A operand is the LayerNorm + SmoothQuant
+// of the f32 rows p.A (K = 384) under `ln` (gamma, beta, smooth), applied in each
+// workgroup's prologue; the workgroups of the first column tile also store the
+// LayerNorm's outputs (ln.dst, and ln.q / ln.scale / ln.rowmax_init* when set).
+// ln.dst must not alias p.A.
+void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st);
+// whether launch_gemm takes the few-rows kernels for m rows (and the prologue form applies)
+bool gemm_small_path(int m);
 
 void launch_row_quant(int m, int n, float* x, const float* smooth, int8_t* q, float* scale, bool gelu,
                       hipStream_t st);
@@ -157,6 +167,7 @@ struct ClsArgs {
   int8_t* act_q_c;         // [B,384]
   float* act_scale_c;      // [B]
   uint32_t* rowmax_init;   // [B] ctx row-absmax buffer to reset
+  uint32_t* rowmax_init2;  // [B] GELU row-absmax buffer to reset, or null
   const float* q_c;        // [B,384]
   const float* kv;         // [T,768]
   float* ctx_c;            // [B,384]
