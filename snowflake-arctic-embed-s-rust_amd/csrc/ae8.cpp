@@ -217,7 +217,7 @@ struct Rng {  // xoshiro256** seeded through SplitMix64
 struct Writer {
   FILE* f;
   bool ok = true;
-  void raw(const void* p, size_t n) { ok = ok && std::fwrite(p, 1, n, f) == n; }
+  void raw(const void* p, size_t n) { ok = ok && (n == 0 || std::fwrite(p, 1, n, f) == n); }
   void u64(uint64_t v) {
     uint8_t b[8];
     for (int i = 0; i < 8; i++) b[i] = uint8_t(v >> (8 * i));
