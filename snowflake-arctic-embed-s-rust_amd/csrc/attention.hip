@@ -219,6 +219,41 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
       score_block(kb + 4, kb8);
     }
   }
+  // PV set-up (phase 6), and the V fragments of its first three key groups and
+  // of the masked tail group, issued now: their latency hides behind the max,
+  // exp and denominator phases instead of opening the PV loop.  Wave w owns the
+  // 16 x 16 output quadrant (query half w/2, dim half w%2).  Group g's V rows are
+  // clamped to the last full group (wave-uniform), so every load is unconditional.
+  const int qh = wave >> 1, dh = wave & 1;
+  const bool has_item = qh < nqh;
+  const int vcol = 2 * H + 16 * dh + lr;
+  // lane part of the V fragment offset (32-bit, from the segment's base)
+  const uint32_t voff = (uint32_t)((kWide ? 4 * lg : lg) * HQKV + vcol);
+  const int Lf = L & ~15, ng = Lf >> 4;
+  const __amdgpu_buffer_rsrc_t vbuf = rows_rsrc(qkv, L);
+  auto load_v = [&](int g, float (&v)[4]) {
+    const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = row_load(vbuf, 4 * voff, t0 + (kWide ? u : 4 * u));
+  };
+  // The last L - Lf (< 16) keys form one more group, masked in phase 6; tail_key(u)
+  // is this lane's key of MFMA u there, its V row clamped per lane.
+  const bool tail = L > Lf;  // wave-uniform
+  auto tail_key = [&](int u) { return Lf + (kWide ? 4 * lg + u : 4 * u + lg); };
+  float v0[4], v1[4], v2[4], vt[4];
+  if (has_item) {
+    if (ng > 0) {
+      load_v(0, v0);
+      load_v(1, v1);
+      load_v(2, v2);
+    }
+    if (tail) {
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        vt[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            vbuf, (uint32_t)(min(tail_key(u), L - 1) * HQKV + vcol) * 4u, 0, 0));
+    }
+  }
 #pragma unroll
   for (int qh = 0; qh < 2; qh++) {
     float m = mrow[qh];
@@ -320,28 +355,15 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   // Lane l ends with queries 16qh + 4lg + i at dim 16dh + lr.  V fragments come
   // from global memory through a register ring.
   __syncthreads();  // publishes s_inv
-  const int qh = wave >> 1, dh = wave & 1;
-  const bool has_item = qh < nqh;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (has_item) {
     // the output's inv_smooth, loaded ahead of the PV loop
     const float sm = p.rowmax ? p.smooth[h * 32 + 16 * dh + lr] : 0.0f;
     const float* prow = &S[(16 * qh + lr) * pitch];
     const float inv = s_inv[16 * qh + lr];
-    const int vcol = 2 * H + 16 * dh + lr;
-    // lane part of the V fragment offset (32-bit, from the segment's base)
-    const uint32_t voff = (uint32_t)((kWide ? 4 * lg : lg) * HQKV + vcol);
     // full groups of 16 keys: no masking.  Group g's V goes to a 4-deep register
-    // ring three groups ahead and its P one group ahead; loads past the last full
-    // group are clamped to it (wave-uniform), so every load is unconditional and
-    // the main loop has no early exit.
-    const int Lf = L & ~15, ng = Lf >> 4;
-    const __amdgpu_buffer_rsrc_t vbuf = rows_rsrc(qkv, L);
-    auto load_v = [&](int g, float (&v)[4]) {
-      const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
-#pragma unroll
-      for (int u = 0; u < 4; u++) v[u] = row_load(vbuf, 4 * voff, t0 + (kWide ? u : 4 * u));
-    };
+    // ring three groups ahead and its P one group ahead (groups 0-2 were loaded
+    // before phase 3), so the main loop has no early exit.
     auto load_p = [&](int g) {
       const float* e = prow + 16 * min(g, ng - 1);
       if constexpr (kWide) {
@@ -371,56 +393,32 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
       const float pu[4] = {e4.x * inv, e4.y * inv, e4.z * inv, e4.w * inv};
       pv_add(pu, v);
     };
-    // The last L - Lf (< 16) keys form one more group, masked: keys past the
-    // segment get p = v = +0, whose +0 products leave the sum unchanged (it
-    // starts at +0, so it is never -0).  Its V is loaded here, before the main
-    // loop, with the rows clamped per lane; tail_key(u) is this lane's key of
-    // MFMA u.
-    const bool tail = L > Lf;  // wave-uniform
-    auto tail_key = [&](int u) { return Lf + (kWide ? 4 * lg + u : 4 * u + lg); };
-    float vt[4];
-    if (tail) {
-#pragma unroll
-      for (int u = 0; u < 4; u++)
-        vt[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            vbuf, (uint32_t)(min(tail_key(u), L - 1) * HQKV + vcol) * 4u, 0, 0));
-    }
+    // The tail group (keys Lf .. L - 1) is masked: keys past the segment get
+    // p = v = +0, whose +0 products leave the sum unchanged (it starts at +0, so
+    // it is never -0).
     if (!kWide) {
       // one group per step through the ring (fewer registers, for short rows)
-      auto load_vn = [&](int g, float (&v)[4]) {
-        const uint32_t t0 = (uint32_t)(16 * min(g, ng - 1));
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = row_load(vbuf, 4 * voff, t0 + 4 * u);
-      };
       auto pv_narrow = [&](int g, const float (&v)[4]) {  // P read as the MFMAs go
 #pragma unroll
         for (int u = 0; u < 4; u++) add_blocks(acc, mfma_products(prow[16 * g + 4 * u + lg] * inv, v[u]));
       };
-      float v0[4], v1[4], v2[4], v3[4];
-      if (ng > 0) {
-        load_vn(0, v0);
-        load_vn(1, v1);
-        load_vn(2, v2);
-      }
+      float v3[4];
       for (int g = 0; g < ng; g += 4) {
-        load_vn(g + 3, v3);
+        load_v(g + 3, v3);
         pv_narrow(g, v0);
         if (g + 1 >= ng) break;
-        load_vn(g + 4, v0);
+        load_v(g + 4, v0);
         pv_narrow(g + 1, v1);
         if (g + 2 >= ng) break;
-        load_vn(g + 5, v1);
+        load_v(g + 5, v1);
         pv_narrow(g + 2, v2);
         if (g + 3 >= ng) break;
-        load_vn(g + 6, v2);
+        load_v(g + 6, v2);
         pv_narrow(g + 3, v3);
       }
     } else if (ng > 0) {
-      float v0[4], v1[4], v2[4], v3[4];
+      float v3[4];
       float4 pa, pb;
-      load_v(0, v0);
-      load_v(1, v1);
-      load_v(2, v2);
       pa = load_p(0);
       int g = 0;
       for (; g + 4 <= ng; g += 4) {

@@ -24,12 +24,16 @@ constexpr float kInvSqrtD = 0.17677669529663687f;  // 1.0f / sqrtf(32.0f), src/m
 // ---------------------------------------------------------------------------
 
 // `(v).round().clamp(-127.0, 127.0) as i8` (f32::round = half away from zero;
-// `as i8` maps NaN to 0).
+// `as i8` maps NaN to 0), as trunc(|v| + (0.5 - 2^-25)) with v's sign, then
+// v_cvt_i32_f32 (saturating, NaN -> 0) and the clamp: the sum rounds up to the
+// next integer exactly when |v| has a fraction >= 0.5.  Equal to the
+// roundf / NaN test / clamp form on all 2^32 inputs (exhaustive CPU check with
+// the conversion's saturation), in five instructions instead of about ten.
 __device__ __forceinline__ int qround(float v) {
-  float r = roundf(v);
-  if (__builtin_isnan(r)) return 0;
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return (int)r;
+  const float r = copysignf(__builtin_truncf(fabsf(v) + 0x1.fffffep-2f), v);
+  int q;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+  return max(-127, min(q, 127));
 }
 
 // qround for |x| <= 127.5 or NaN, which holds wherever x = v * (127 / max_abs)
@@ -211,12 +215,19 @@ __device__ __forceinline__ float lds_row_sum(const float* row, F f) {
       acc += f(v[i].x); acc += f(v[i].y); acc += f(v[i].z); acc += f(v[i].w);
     }
   };
+  // sched_barrier: keep each batch's reads issued before the previous batch's
+  // adds (the scheduler would otherwise gather both batches' reads at the top of
+  // the loop and expose the LDS latency once per iteration)
   ld(0, va);
   for (int bi = 0; bi < 12; bi += 2) {
     ld(bi + 1, vb);
+    __builtin_amdgcn_sched_barrier(0);
     add(va);
+    __builtin_amdgcn_sched_barrier(0);
     ld(bi + 2, va);
+    __builtin_amdgcn_sched_barrier(0);
     add(vb);
+    __builtin_amdgcn_sched_barrier(0);
   }
   return acc;
 }

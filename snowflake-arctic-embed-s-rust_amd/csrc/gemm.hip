@@ -256,30 +256,39 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
 
 // ---------------------------------------------------------------------------
 // Small M (latency-bound launches: single sequences, short batches, the
-// layer-11 tail): 16 rows per workgroup, four times the workgroups of the
-// 64-row tiles.  The workgroup stages its whole A tile (16 x K int8; f32 A is
-// quantized on the way, as astore does above) into LDS once, so the K loop has
-// no barrier; each wave streams its B fragments through a register ring
-// kRing K steps deep, which hides the L2 latency of those loads.  The residual
-// rows are loaded before the K loop.  Each wave owns 48 columns; with 8 waves
-// the workgroup spans all 384 columns, and with LN it applies the LayerNorm +
-// SmoothQuant of `ln` to its 16 output rows (layernorm_smooth_quantize_row_scalar,
-// reference src/simd_math.rs:208-247; p.out is then not written).
+// layer-11 tail): 16 rows per workgroup of 8 waves.  The workgroup stages its
+// whole A tile (16 x K int8; f32 A is quantized on the way, as astore does
+// above; kALn: through a LayerNorm) into LDS once, so the K loop has no
+// barrier; each wave streams its B fragments through a register ring kRing K
+// steps deep.
+//
+// The 8 waves form CG = 8 / KS column groups of 48 columns, and the KS waves of
+// a group split K: wave w takes column group w % CG and K steps
+// [(w / CG) KT / KS, (w / CG + 1) KT / KS).  Their int32 partial sums (exact in
+// any order) meet in LDS, and each of them applies the epilogue to 16 / KS of
+// the 16 rows.  KS = 1: the workgroup spans 384 columns (with LN it applies the
+// LayerNorm + SmoothQuant of `ln` to its 16 output rows, reference
+// src/simd_math.rs:208-247, and p.out is not written); KS = 2: 192 columns;
+// KS = 8: 48 columns, for long K (a workgroup streams an eighth of the weights
+// of the KS = 1 form).
 // ---------------------------------------------------------------------------
 constexpr int kSmallMaxK = 1536;
 constexpr int kSmallPitch = kSmallMaxK + 16;  // LDS bytes per A row: conflict-free fragment reads
 constexpr int kLnPitchS = 388;                // LDS floats per row of the fused LayerNorm
+constexpr int kEPitchS = 52;                  // LDS words per row of a wave's epilogue staging tile
 
-template <int AM, int EM, int WAVES, bool LN>
-__global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnArgs ln) {
-  constexpr int NW = 48, kThreads = 64 * WAVES;
-  constexpr int kBN = WAVES * NW, kCB = NW / 16, kF4 = NW / 4, kEk = kF4 / 4;
+template <int AM, int EM, bool LN, int KS>
+__global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) {
+  constexpr int WAVES = 8, NW = 48, kThreads = 512;
+  constexpr int CG = WAVES / KS, kBN = CG * NW, kCB = NW / 16, kF4 = NW / 4;
+  constexpr int RPW = 16 / KS, kPos = RPW * kF4, kEk = (kPos + 63) / 64;  // epilogue rows / float4s per wave
   constexpr int kRing = 8;
-  static_assert(!LN || (WAVES == 8 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
-  static_assert(AM != kALn || (WAVES == 4 && !LN), "LayerNorm prologue: 256 threads, 16 per row");
+  static_assert(KS == 1 || KS == 2 || KS == 8, "K splits");
+  static_assert(!LN || (KS == 1 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
+  static_assert(AM != kALn || !LN, "LayerNorm prologue or epilogue");
   constexpr bool kLnTile = LN || AM == kALn;  // an f32 row tile for a LayerNorm
   __shared__ __attribute__((aligned(16))) int8_t sA[16 * kSmallPitch];
-  __shared__ __attribute__((aligned(16))) int sE[WAVES][16 * kEPitch];
+  __shared__ __attribute__((aligned(16))) int sE[WAVES][16 * kEPitchS];
   static_assert(!kLnTile || sizeof(sE) >= 16 * kLnPitchS * sizeof(float), "LN squares reuse the staging tile");
   __shared__ uint32_t sRowMax[WAVES][16];
   __shared__ __attribute__((aligned(16))) float sEpSa[16], sEpWs[kBN], sEpB[kBN];
@@ -289,17 +298,67 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
   const int fr = lane & 15, fk = (lane >> 4) * 16;
   const int mt = (p.M + 15) >> 4;
   const int m0 = (blockIdx.x % mt) * 16, n0 = (blockIdx.x / mt) * kBN;
-  const int KT = p.K >> 6, NB = p.N >> 4;
-  const int col0 = n0 + wave * NW;
+  const int NB = p.N >> 4;
+  const int cg = wave % CG, ks = wave / CG;
+  const int col0 = n0 + cg * NW;
+  // this wave's K steps [kb0, kb0 + KT)
+  const int KT = (p.K >> 6) / KS, kb0 = ks * KT;
   const ExpTab tb = exp_tab_regs();  // the epilogue below is wave-uniform
 
-  // B ring: the first kRing K steps, issued first
+  // The A tile's global loads go out first, then the B ring and the epilogue
+  // operands: memory operations retire in order, so the wait for A does not wait
+  // for the weights.  The A tile is 16 rows x K as 16-byte chunks (16 k-values);
+  // thread t takes chunks t + 512 i (kALn: f32 columns 4 (sub + 32 i) .. +3 of
+  // row tid / 32).
+  constexpr int kChunks = 16 * kSmallMaxK / 16 / kThreads;  // per thread at the largest K
+  const int cpr = p.K >> 4, nch = 16 * cpr;                // chunks per row, in the tile
+  const int rr = tid >> 5, sub = tid & 31, lrow = m0 + rr;  // kALn: row and column group
+  float4 xv[3], lg[3], lb[3], lsm[3];                       // kALn: x, gamma, beta, inv_smooth
+  v4i qa[kChunks];                                          // kAI8
+  float4 xa[kChunks][4];                                    // f32 A
+  float a_inv[kChunks];
+  if constexpr (AM == kALn) {
+    const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)min(lrow, p.M - 1) * 384;
+#pragma unroll
+    for (int i = 0; i < 3; i++) xv[i] = *reinterpret_cast<const float4*>(xr + (sub + 32 * i) * 4);
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      lg[i] = *reinterpret_cast<const float4*>(ln.gamma + c);
+      lb[i] = *reinterpret_cast<const float4*>(ln.beta + c);
+      lsm[i] = *reinterpret_cast<const float4*>(ln.smooth + c);
+    }
+  } else if constexpr (AM == kAI8) {
+#pragma unroll
+    for (int i = 0; i < kChunks; i++) {
+      const int c = tid + kThreads * i, r = c / cpr;
+      if (c < nch)
+        qa[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(p.A) +
+                                              (size_t)min(m0 + r, p.M - 1) * p.K + (c - r * cpr) * 16);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kChunks; i++) {
+      const int c = tid + kThreads * i, r = c / cpr;
+      if (c < nch) {
+        const int row = min(m0 + r, p.M - 1);
+        const float4* src =
+            reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.A) + (size_t)row * p.K + (c - r * cpr) * 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) xa[i][k] = src[k];
+        a_inv[i] = __uint_as_float(p.a_rowmax[row]);
+      }
+    }
+  }
+
+  // B ring: the first kRing K steps
   const int cb0 = col0 >> 4;
   const int8_t* wbase = p.w + (size_t)lane * 16;
   v4i bring[kRing][kCB];
   auto bload = [&](int kt, v4i (&dst)[kCB]) {
 #pragma unroll
-    for (int j = 0; j < kCB; j++) dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + cb0 + j) * 1024);
+    for (int j = 0; j < kCB; j++)
+      dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)(kb0 + kt) * NB + cb0 + j) * 1024);
   };
 #pragma unroll
   for (int u = 0; u < kRing; u++)
@@ -315,141 +374,111 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
   } else if (tid < 16 + kBN / 2) {
     ep_reg = reinterpret_cast<const float4*>(p.bias + n0)[tid - 16 - kBN / 4];
   }
-  // residual float4s of this lane's epilogue positions
+  // Epilogue position k of this lane: float4 e = lane + 64 k of the wave's
+  // RPW x kF4 block (clamped to the last one, so that every lane runs the
+  // wave-uniform GELU), row ks * RPW + e / kF4, columns col0 + 4 (e % kF4).
+  auto epos = [&](int k, int& er, int& ec4) {
+    const int e = min(lane + 64 * k, kPos - 1);
+    er = ks * RPW + e / kF4;
+    ec4 = e % kF4;
+  };
   float4 resv[kEk];
   if (p.res) {
 #pragma unroll
     for (int k = 0; k < kEk; k++) {
-      const int idx = lane + 64 * k;
-      const int row = min(m0 + idx / kF4, p.M - 1);
-      resv[k] = *reinterpret_cast<const float4*>(p.res + (size_t)row * p.N + col0 + (idx % kF4) * 4);
+      int er, ec4;
+      epos(k, er, ec4);
+      resv[k] = *reinterpret_cast<const float4*>(p.res + (size_t)min(m0 + er, p.M - 1) * p.N + col0 + ec4 * 4);
     }
   }
-  // the A tile: 16 rows x K as 16-byte chunks (16 k-values); thread t takes
-  // chunks t + kThreads * i.  Every load is issued before any is used (one
-  // round trip), then f32 A is quantized as astore does above.
-  {
-    constexpr int kChunks = 16 * kSmallMaxK / 16 / kThreads;  // per thread at the largest K
-    const int cpr = p.K >> 4, nch = 16 * cpr;            // chunks per row, in the tile
-    if constexpr (AM == kALn) {
-      // LayerNorm + SmoothQuant of the 16 rows (layernorm_smooth_quantize_row_scalar,
-      // reference src/simd_math.rs:208-247, as ln_quant_kernel computes it): one
-      // lane per row takes the in-order sums, 16 threads per row the rest; the
-      // int8 result is the A tile and its scale the epilogue's row scale.
-      const int rr = tid >> 4, sub = tid & 15, row = m0 + rr;
-      const bool writer = n0 == 0 && row < p.M;
-      const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)min(row, p.M - 1) * 384;
-      float4 xv[6], g[6], b[6], sm[6];
+
+  // the A tile into LDS: int8 A as loaded, f32 A quantized as astore does above,
+  // kALn through the LayerNorm
+  if constexpr (AM == kALn) {
+    // LayerNorm + SmoothQuant of the 16 rows (layernorm_smooth_quantize_row_scalar,
+    // reference src/simd_math.rs:208-247, as ln_quant_kernel computes it): one
+    // lane per row takes the in-order sums, 32 threads per row the rest; the
+    // int8 result is the A tile and its scale the epilogue's row scale.
+    const bool writer = n0 == 0 && lrow < p.M;
 #pragma unroll
-      for (int i = 0; i < 6; i++) {
-        const int c = (sub + 16 * i) * 4;
-        xv[i] = *reinterpret_cast<const float4*>(xr + c);
-        g[i] = *reinterpret_cast<const float4*>(ln.gamma + c);
-        b[i] = *reinterpret_cast<const float4*>(ln.beta + c);
-        sm[i] = *reinterpret_cast<const float4*>(ln.smooth + c);
+    for (int i = 0; i < 3; i++) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + (sub + 32 * i) * 4]) = xv[i];
+    __syncthreads();
+    if (tid < 16) s_stat[0][tid] = lds_row_sum(&sLn[tid * kLnPitchS], [](float x) { return x; }) / 384.0f;
+    __syncthreads();
+    const float mean = s_stat[0][rr];
+    float* sSq = reinterpret_cast<float*>(&sE[0][0]);  // (x - mean)^2 rows; the staging tile is free until the epilogue
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      float4 d = xv[i];
+      d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+      *reinterpret_cast<float4*>(&sSq[rr * kLnPitchS + (sub + 32 * i) * 4]) =
+          make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
+    }
+    __syncthreads();
+    if (tid < 16)
+      s_stat[1][tid] = 1.0f / sqrtf(lds_row_sum(&sSq[tid * kLnPitchS], [](float x) { return x; }) / 384.0f + 1e-12f);
+    __syncthreads();
+    const float rstd = s_stat[1][rr];
+    float4 ys[3];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      float4 y;
+      y.x = (xv[i].x - mean) * rstd * lg[i].x + lb[i].x;
+      y.y = (xv[i].y - mean) * rstd * lg[i].y + lb[i].y;
+      y.z = (xv[i].z - mean) * rstd * lg[i].z + lb[i].z;
+      y.w = (xv[i].w - mean) * rstd * lg[i].w + lb[i].w;
+      if (writer) *reinterpret_cast<float4*>(ln.dst + (size_t)lrow * 384 + c) = y;
+      ys[i] = make_float4(y.x * lsm[i].x, y.y * lsm[i].y, y.z * lsm[i].z, y.w * lsm[i].w);
+      amax = nanless_max(amax, fabsf(ys[i].x));
+      amax = nanless_max(amax, fabsf(ys[i].y));
+      amax = nanless_max(amax, fabsf(ys[i].z));
+      amax = nanless_max(amax, fabsf(ys[i].w));
+    }
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+    const float max_abs = nanless_max(1e-8f, amax);
+    const float inv_scale = 127.0f / max_abs;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int c = (sub + 32 * i) * 4;
+      const uint32_t q4 = pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale),
+                                qround(ys[i].z * inv_scale), qround(ys[i].w * inv_scale));
+      *reinterpret_cast<uint32_t*>(&sA[rr * kSmallPitch + c]) = q4;
+      if (writer && ln.q) *reinterpret_cast<uint32_t*>(ln.q + (size_t)lrow * 384 + c) = q4;
+    }
+    if (sub == 0) {
+      sEpSa[rr] = max_abs / 127.0f;
+      if (writer) {
+        if (ln.scale) ln.scale[lrow] = max_abs / 127.0f;
+        if (ln.rowmax_init) ln.rowmax_init[lrow] = __float_as_uint(1e-8f);
+        if (ln.rowmax_init2) ln.rowmax_init2[lrow] = __float_as_uint(1e-8f);
       }
+    }
+  } else if constexpr (AM == kAI8) {
 #pragma unroll
-      for (int i = 0; i < 6; i++) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + (sub + 16 * i) * 4]) = xv[i];
-      __syncthreads();
-      if (tid < 16) s_stat[0][tid] = lds_row_sum(&sLn[tid * kLnPitchS], [](float x) { return x; }) / 384.0f;
-      __syncthreads();
-      const float mean = s_stat[0][rr];
-      float* sSq = reinterpret_cast<float*>(&sE[0][0]);  // (x - mean)^2 rows; the staging tile is free until the epilogue
+    for (int i = 0; i < kChunks; i++) {
+      const int c = tid + kThreads * i, r = c / cpr;
+      if (c < nch) *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + (c - r * cpr) * 16]) = qa[i];
+    }
+  } else {
 #pragma unroll
-      for (int i = 0; i < 6; i++) {
-        float4 d = xv[i];
-        d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
-        *reinterpret_cast<float4*>(&sSq[rr * kLnPitchS + (sub + 16 * i) * 4]) =
-            make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
-      }
-      __syncthreads();
-      if (tid < 16)
-        s_stat[1][tid] = 1.0f / sqrtf(lds_row_sum(&sSq[tid * kLnPitchS], [](float x) { return x; }) / 384.0f + 1e-12f);
-      __syncthreads();
-      const float rstd = s_stat[1][rr];
-      float4 ys[6];
-      float amax = 0.0f;
+    for (int i = 0; i < kChunks; i++) {
+      const int c = tid + kThreads * i, r = c / cpr, kc = (c - r * cpr) * 16;
+      if (c < nch) {
+        const float inv = 127.0f / a_inv[i];  // inv_scale = 127.0 / max_abs
+        uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 6; i++) {
-        const int c = (sub + 16 * i) * 4;
-        float4 y;
-        y.x = (xv[i].x - mean) * rstd * g[i].x + b[i].x;
-        y.y = (xv[i].y - mean) * rstd * g[i].y + b[i].y;
-        y.z = (xv[i].z - mean) * rstd * g[i].z + b[i].z;
-        y.w = (xv[i].w - mean) * rstd * g[i].w + b[i].w;
-        if (writer) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + c) = y;
-        ys[i] = make_float4(y.x * sm[i].x, y.y * sm[i].y, y.z * sm[i].z, y.w * sm[i].w);
-        amax = nanless_max(amax, fabsf(ys[i].x));
-        amax = nanless_max(amax, fabsf(ys[i].y));
-        amax = nanless_max(amax, fabsf(ys[i].z));
-        amax = nanless_max(amax, fabsf(ys[i].w));
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
-      const float max_abs = nanless_max(1e-8f, amax);
-      const float inv_scale = 127.0f / max_abs;
-#pragma unroll
-      for (int i = 0; i < 6; i++) {
-        const int c = (sub + 16 * i) * 4;
-        const uint32_t q4 = pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale),
-                                  qround(ys[i].z * inv_scale), qround(ys[i].w * inv_scale));
-        *reinterpret_cast<uint32_t*>(&sA[rr * kSmallPitch + c]) = q4;
-        if (writer && ln.q) *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + c) = q4;
-      }
-      if (sub == 0) {
-        sEpSa[rr] = max_abs / 127.0f;
-        if (writer) {
-          if (ln.scale) ln.scale[row] = max_abs / 127.0f;
-          if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
-          if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
-        }
-      }
-    } else if constexpr (AM == kAI8) {
-      v4i q[kChunks];
-#pragma unroll
-      for (int i = 0; i < kChunks; i++) {
-        const int c = tid + kThreads * i, r = c / cpr;
-        if (c < nch)
-          q[i] = *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(p.A) +
-                                               (size_t)min(m0 + r, p.M - 1) * p.K + (c - r * cpr) * 16);
-      }
-#pragma unroll
-      for (int i = 0; i < kChunks; i++) {
-        const int c = tid + kThreads * i, r = c / cpr;
-        if (c < nch) *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + (c - r * cpr) * 16]) = q[i];
-      }
-    } else {
-      float4 x[kChunks][4];
-      float a_inv[kChunks];
-#pragma unroll
-      for (int i = 0; i < kChunks; i++) {
-        const int c = tid + kThreads * i, r = c / cpr;
-        if (c < nch) {
-          const int row = min(m0 + r, p.M - 1);
-          const float4* src =
-              reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p.A) + (size_t)row * p.K + (c - r * cpr) * 16);
-#pragma unroll
-          for (int k = 0; k < 4; k++) x[i][k] = src[k];
-          a_inv[i] = __uint_as_float(p.a_rowmax[row]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kChunks; i++) {
-        const int c = tid + kThreads * i, r = c / cpr, kc = (c - r * cpr) * 16;
-        if (c < nch) {
-          const float inv = 127.0f / a_inv[i];  // inv_scale = 127.0 / max_abs
-          uint32_t w[4];
-#pragma unroll
-          for (int k = 0; k < 4; k++) {
-            float4 v = x[i][k];
-            if (AM == kAF32QSmooth) {  // (x * inv_smooth[j]) * inv_scale
-              const float4 sm = reinterpret_cast<const float4*>(p.a_smooth + kc)[k];
-              v.x = v.x * sm.x; v.y = v.y * sm.y; v.z = v.z * sm.z; v.w = v.w * sm.w;
-            }
-            w[k] = pack4(qround(v.x * inv), qround(v.y * inv), qround(v.z * inv), qround(v.w * inv));
+        for (int k = 0; k < 4; k++) {
+          float4 v = xa[i][k];
+          if (AM == kAF32QSmooth) {  // (x * inv_smooth[j]) * inv_scale
+            const float4 sm = reinterpret_cast<const float4*>(p.a_smooth + kc)[k];
+            v.x = v.x * sm.x; v.y = v.y * sm.y; v.z = v.z * sm.z; v.w = v.w * sm.w;
           }
-          *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + kc]) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+          w[k] = pack4(qround(v.x * inv), qround(v.y * inv), qround(v.z * inv), qround(v.w * inv));
         }
+        *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + kc]) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
       }
     }
   }
@@ -470,7 +499,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
     for (int u = 0; u < kRing; u++) {
       const int kt = k0 + u;
       if (kt < KT) {  // wave-uniform
-        const v4i af = *reinterpret_cast<const v4i*>(&sA[fr * kSmallPitch + kt * 64 + fk]);
+        const v4i af = *reinterpret_cast<const v4i*>(&sA[fr * kSmallPitch + (kb0 + kt) * 64 + fk]);
 #pragma unroll
         for (int j = 0; j < kCB; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bring[u][j], acc[j], 0, 0, 0);
         if (kt + kRing < KT) bload(kt + kRing, bring[u]);
@@ -478,22 +507,34 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
     }
   }
 
-  // epilogue: the accumulators through this wave's LDS tile, then whole rows
-  int* E = sE[wave];
+  // epilogue: every wave's accumulators through its LDS tile; each wave then
+  // adds its column group's KS partial tiles for its rows and writes whole
+  // float4s
+  {
+    int* E = sE[wave];
 #pragma unroll
-  for (int j = 0; j < kCB; j++)
+    for (int j = 0; j < kCB; j++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[j][r];
+      for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitchS + j * 16 + fr] = acc[j][r];
+  }
   if (EM == kEpiGelu && lane < 16) sRowMax[wave][lane] = 0u;
-  wave_lds_sync();  // E and sRowMax are private to this wave
+  if constexpr (KS > 1) __syncthreads();  // the partial tiles of the other waves
+  else wave_lds_sync();                   // E and sRowMax are private to this wave
 #pragma unroll
-  for (int k = 0; k < kEk; k++) {  // 16 rows x kF4 float4 over 64 lanes
-    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
-    const int row = m0 + rr, col = col0 + c4 * 4;
-    const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
-    const float sa = sEpSa[rr];
-    const float4 ws4 = *reinterpret_cast<const float4*>(&sEpWs[wave * NW + c4 * 4]);
-    float4 b4 = *reinterpret_cast<const float4*>(&sEpB[wave * NW + c4 * 4]);
+  for (int k = 0; k < kEk; k++) {
+    int er, c4;
+    epos(k, er, c4);
+    const bool valid = lane + 64 * k < kPos;  // wave-uniform in k; per lane at the last k
+    const int row = m0 + er, col = col0 + c4 * 4;
+    int4 a4 = *reinterpret_cast<const int4*>(&sE[cg][er * kEPitchS + c4 * 4]);
+#pragma unroll
+    for (int s2 = 1; s2 < KS; s2++) {
+      const int4 b = *reinterpret_cast<const int4*>(&sE[cg + CG * s2][er * kEPitchS + c4 * 4]);
+      a4.x += b.x; a4.y += b.y; a4.z += b.z; a4.w += b.w;
+    }
+    const float sa = sEpSa[er];
+    const float4 ws4 = *reinterpret_cast<const float4*>(&sEpWs[cg * NW + c4 * 4]);
+    float4 b4 = *reinterpret_cast<const float4*>(&sEpB[cg * NW + c4 * 4]);
     if (p.res) {
       b4.x = b4.x + resv[k].x; b4.y = b4.y + resv[k].y; b4.z = b4.z + resv[k].z; b4.w = b4.w + resv[k].w;
     }
@@ -509,13 +550,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_small_kernel(GemmArgs p, LnAr
       v.z = gelu_exact(v.z, tb) * g4.z;
       v.w = gelu_exact(v.w, tb) * g4.w;
       float gm = nanless_max(nanless_max(fabsf(v.x), fabsf(v.y)), nanless_max(fabsf(v.z), fabsf(v.w)));
-      atomicMax(&sRowMax[wave][rr], __float_as_uint(gm));  // non-negative f32 bits order like u32
+      if (valid) atomicMax(&sRowMax[wave][er - ks * RPW], __float_as_uint(gm));  // non-negative f32 bits order like u32
     }
-    if constexpr (LN) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + col]) = v;
-    else if (row < p.M) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
+    if constexpr (LN) *reinterpret_cast<float4*>(&sLn[er * kLnPitchS + col]) = v;
+    else if (valid && row < p.M) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
   }
   wave_lds_sync();
-  if (EM == kEpiGelu && lane < 16 && m0 + lane < p.M) atomicMax(&p.g_rowmax[m0 + lane], sRowMax[wave][lane]);
+  if (EM == kEpiGelu && lane < RPW && m0 + ks * RPW + lane < p.M)
+    atomicMax(&p.g_rowmax[m0 + ks * RPW + lane], sRowMax[wave][lane]);
   if constexpr (LN) {
     // sequential sums per row (one lane each), then 32 lanes per row normalize
     // and quantize; ln.dst may equal p.res (its rows were loaded above)
@@ -597,7 +639,11 @@ constexpr int kSmallM = 1024;
 // tile fastest, 25 MB at M = 65,536 up to 13 % slower)
 constexpr size_t kColFastABytes = size_t(96) << 20;
 
-static bool small_gemm(const GemmArgs& p) { return p.M <= kSmallM && p.K <= kSmallMaxK; }
+// (the K-split forms need an even number of 64-deep K steps)
+static bool small_gemm(const GemmArgs& p) { return p.M <= kSmallM && p.K <= kSmallMaxK && p.K % 128 == 0; }
+// From this K on (a multiple of 512), a small-M f32-epilogue GEMM splits K over
+// the 8 waves of 16 x 48 workgroups (gemm_small_kernel KS = 8)
+constexpr int kSplitMinK = 1024;
 
 // ln != null: N = 384, kEpiF32, small_gemm(p); the epilogue applies *ln to each
 // output row and p.out is not written
@@ -605,9 +651,15 @@ template <int AM, int EM>
 static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullptr) {
   const int mt16 = (p.M + 15) / 16;
   if (small_gemm(p)) {
-    if (ln) hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, 8, true>), dim3(mt16), dim3(512), 0, st, p, *ln);
-    else hipLaunchKernelGGL((gemm_small_kernel<AM, EM, 4, false>), dim3(mt16 * (p.N / 192)), dim3(256), 0, st, p,
-                            LnArgs{});
+    if (ln) {
+      hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, true, 1>), dim3(mt16), dim3(512), 0, st, p, *ln);
+    } else if (EM == kEpiF32 && p.K >= kSplitMinK && p.K % 512 == 0) {
+      hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, false, 8>), dim3(mt16 * (p.N / 48)), dim3(512), 0, st, p,
+                         LnArgs{});
+    } else {
+      hipLaunchKernelGGL((gemm_small_kernel<AM, EM, false, 2>), dim3(mt16 * (p.N / 192)), dim3(512), 0, st, p,
+                         LnArgs{});
+    }
     return;
   }
   p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;
@@ -622,8 +674,8 @@ bool gemm_small_path(int m) { return m > 0 && m <= kSmallM; }
 void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st) {
   if (p.M <= 0 || p.M > kSmallM || p.K != 384) return;
   const dim3 grid(((p.M + 15) / 16) * (p.N / 192));
-  if (emode == kEpiGelu) hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, 4, false>), grid, dim3(256), 0, st, p, ln);
-  else hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, 4, false>), grid, dim3(256), 0, st, p, ln);
+  if (emode == kEpiGelu) hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, false, 2>), grid, dim3(512), 0, st, p, ln);
+  else hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, false, 2>), grid, dim3(512), 0, st, p, ln);
 }
 
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {

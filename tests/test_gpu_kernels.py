@@ -12,7 +12,10 @@ import oracle as orc
 
 pytestmark = pytest.mark.gpu
 f32 = np.float32
-SHAPES = [(1152, 384), (384, 384), (1536, 384), (384, 1536), (768, 384)]
+# (n, k): the model's four, plus K = 1152 (an even number of 64-deep K steps off
+# the model's sizes) and K = 448 (an odd number: the small-M forms hand it to the
+# tiled kernel)
+SHAPES = [(1152, 384), (384, 384), (1536, 384), (384, 1536), (768, 384), (384, 1152), (384, 448)]
 
 
 def dev(torch, a):
