@@ -643,6 +643,8 @@ int attention_pitch(int max_len) {
   return ((L + 15) / 16) * 16 + 4;
 }
 
+__global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p);
+
 // allow > 64 KiB of dynamic LDS for the tiled kernel on the current device; called
 // at engine open and by the stand-alone operator, never inside a stream capture
 void init_attention_kernels() {
@@ -651,6 +653,8 @@ void init_attention_kernels() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(cls_attention_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sizeof(float) * 32 * 512));
 }
 
 // The wide variant (3 workgroups per CU by registers) is faster from rows of
@@ -743,69 +747,123 @@ __global__ __launch_bounds__(128) void gather_cls_kernel(ClsArgs p) {
   }
 }
 
-// one wave per (sequence, head): the [CLS] query attends to its segment with the
-// same exact scalar order as attention_kernel (src/model.rs:814-843)
-__global__ __launch_bounds__(64) void cls_attention_kernel(ClsArgs p) {
+// one workgroup (4 waves) per (sequence, head): the [CLS] query attends to its
+// segment with the same exact scalar order as attention_kernel
+// (src/model.rs:814-843).  Every global load is issued at the start: the K rows
+// of the thread's keys (tid, tid + 256) and the segment's V rows, which go to LDS
+// ([key][32], dynamic, p.max_len keys) for the in-order PV sums.  Keys past
+// p.max_len (<= 512) are not attended (the embedding kernel reports such
+// sequences through the workspace's error word).
+__global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
+  extern __shared__ __attribute__((aligned(16))) float sV[];  // [L][32]
   __shared__ __attribute__((aligned(16))) float S[512];
+  __shared__ float s_m[4];
   __shared__ float s_inv;
-  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, 512);
+  const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, p.max_len);
   const ExpTab tb = exp_tab_regs();
+  // V: float4 f = tid + 256 i is key f / 8, dims 4 (f % 8) .. +3
+  constexpr int kVF = 512 * 8 / 256;
+  float4 vr[kVF];
+#pragma unroll
+  for (int i = 0; i < kVF; i++) {
+    const int f = tid + 256 * i;
+    if (f < 8 * L) vr[i] = *reinterpret_cast<const float4*>(p.kv + (size_t)(s0 + f / 8) * 2 * H + H + h * 32 + (f % 8) * 4);
+  }
+  float4 kr[2][8];
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int j = tid + 256 * u;
+    if (j < L) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) kr[u][e] = *reinterpret_cast<const float4*>(p.kv + (size_t)(s0 + j) * 2 * H + h * 32 + 4 * e);
+    }
+  }
   float q[32];
 #pragma unroll
   for (int d = 0; d < 32; d += 4) {
     const float4 v = *reinterpret_cast<const float4*>(p.q_c + (size_t)b * H + h * 32 + d);
     q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
   }
-  float m = -INFINITY;
-  for (int j = lane; j < L; j += 64) {
-    const float* kr = p.kv + (size_t)(s0 + j) * 2 * H + h * 32;
-    float sum = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 32; e += 4) {
-      const float4 k = *reinterpret_cast<const float4*>(kr + e);
-      sum += q[e] * k.x;
-      sum += q[e + 1] * k.y;
-      sum += q[e + 2] * k.z;
-      sum += q[e + 3] * k.w;
+  for (int i = 0; i < kVF; i++) {
+    const int f = tid + 256 * i;
+    if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
+  }
+  // scores (dot32_f32 order) and their max
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    const int j = tid + 256 * u;
+    if (j < L) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        sum += q[4 * e] * kr[u][e].x;
+        sum += q[4 * e + 1] * kr[u][e].y;
+        sum += q[4 * e + 2] * kr[u][e].z;
+        sum += q[4 * e + 3] * kr[u][e].w;
+      }
+      const float sc = sum * kInvSqrtD;
+      S[j] = sc;
+      m = nanless_max(m, sc);
     }
-    const float sc = sum * kInvSqrtD;
-    S[j] = sc;
-    m = nanless_max(m, sc);
   }
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
+  if (lane == 0) s_m[wave] = m;
   __syncthreads();
-  for (int j0 = 0; j0 < L; j0 += 64) {  // wave-uniform trip count (expf_libm needs all lanes)
-    const int j = j0 + lane;
+  m = nanless_max(nanless_max(s_m[0], s_m[1]), nanless_max(s_m[2], s_m[3]));
+#pragma unroll
+  for (int u = 0; u < 2; u++) {  // uniform trip count (expf_libm needs all lanes)
+    const int j = tid + 256 * u;
     const float e = expf_libm((j < L ? S[j] : 0.0f) - m, tb);
     if (j < L) S[j] = e;
   }
   __syncthreads();
-  if (lane == 0) {
+  if (tid == 0) {  // in-order denominator
     float sum = 0.0f;
-    for (int j = 0; j < L; j++) sum += S[j];
+    int j = 0;
+    for (; j + 4 <= L; j += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(&S[j]);
+      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    }
+    for (; j < L; j++) sum += S[j];
     s_inv = 1.0f / sum;
   }
   __syncthreads();
   const float inv = s_inv;
-  for (int j = lane; j < L; j += 64) S[j] = S[j] * inv;
-  __syncthreads();
-  float o = 0.0f;
-  if (lane < 32) {
-    const float* vr = p.kv + (size_t)s0 * 2 * H + H + h * 32 + lane;
-    for (int t = 0; t < L; t++) o = o + S[t] * vr[(size_t)t * 2 * H];
-    p.ctx_c[(size_t)b * H + h * 32 + lane] = o;
-  }
-  float a = lane < 32 ? fabsf(o * p.smooth[h * 32 + lane]) : 0.0f;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
-  if (lane == 0) atomicMax(&p.rowmax_ctx_c[b], __float_as_uint(a));
+  for (int u = 0; u < 2; u++) {
+    const int j = tid + 256 * u;
+    if (j < L) S[j] = S[j] * inv;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float o = 0.0f;
+    if (lane < 32) {  // ctx_d = sum_t p_t * v_t,d in order
+      int t = 0;
+      for (; t + 4 <= L; t += 4) {
+        const float4 pt = *reinterpret_cast<const float4*>(&S[t]);
+        o = o + pt.x * sV[32 * t + lane];
+        o = o + pt.y * sV[32 * (t + 1) + lane];
+        o = o + pt.z * sV[32 * (t + 2) + lane];
+        o = o + pt.w * sV[32 * (t + 3) + lane];
+      }
+      for (; t < L; t++) o = o + S[t] * sV[32 * t + lane];
+      p.ctx_c[(size_t)b * H + h * 32 + lane] = o;
+    }
+    float a = lane < 32 ? fabsf(o * p.smooth[h * 32 + lane]) : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
+    if (lane == 0) atomicMax(&p.rowmax_ctx_c[b], __float_as_uint(a));
+  }
 }
 
 void launch_cls(const ClsArgs& p, int stage, hipStream_t st) {
   if (stage == 0) hipLaunchKernelGGL(gather_cls_kernel, dim3(p.B), dim3(128), 0, st, p);
-  else if (stage == 1) hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(64), 0, st, p);
+  else if (stage == 1)
+    hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), sizeof(float) * 32 * (size_t)p.max_len, st, p);
 }
 
 }  // namespace aek

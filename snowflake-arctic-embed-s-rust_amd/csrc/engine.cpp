@@ -528,6 +528,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   c.ctx_c = ws->ctx_c;
   c.smooth = D.attn_out.inv_smooth;
   c.rowmax_ctx_c = ws->rowmax_ctx_c;
+  c.max_len = std::min(max_len, ae::kMaxPos);
   launch_cls(c, 0, st);
   gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
   launch_cls(c, 1, st);

@@ -173,6 +173,7 @@ struct ClsArgs {
   float* ctx_c;            // [B,384]
   const float* smooth;     // attn_out inv_smooth
   uint32_t* rowmax_ctx_c;  // [B]
+  int max_len = 512;       // keys attended per sequence (<= 512): sizes the V tile in LDS
 };
 void launch_cls(const ClsArgs& p, int stage, hipStream_t st);
 void launch_final_ln_l2(int B, const float* src, const float* gamma, const float* beta, float* out, hipStream_t st);
