@@ -289,6 +289,11 @@ int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream);
  * floats).  out_dev[(set*64 + lane)*16 + r] = a[set*64 + blk*16 + m] *
  * b[set*64 + blk*16 + n] with blk = r/4, m = 4*(lane/16) + r%4, n = lane%16. */
 int ae_debug_mfma_products(const float* a_dev, const float* b_dev, float* out_dev, int n_sets, void* stream);
+/* Which exact-attention kernels the library launches, process-wide (a test
+ * hook, no reference counterpart): 0 by the batch's shape (the default), 1 the
+ * tiled and register-row kernels only, 2 the latency form only.  Every form
+ * gives the same bits.  AE_ERR_INVALID_ARG for another value. */
+int ae_debug_set_attention_form(int form);
 
 #ifdef __cplusplus
 }

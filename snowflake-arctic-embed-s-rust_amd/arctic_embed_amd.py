@@ -77,6 +77,7 @@ _SIGS = {
     "ae_tokenizer_vocab_size": (_sz, [_vp]),
     "ae_debug_gelu_map": (_i32, [_vp, _vp, _sz, _vp]),
     "ae_debug_mfma_products": (_i32, [_vp, _vp, _vp, ctypes.c_int, _vp]),
+    "ae_debug_set_attention_form": (_i32, [ctypes.c_int]),
     "ae_workspace_set_timing": (_i32, [_vp, _i32]),
     "ae_workspace_set_graphs": (_i32, [_vp, _i32]),
     "ae_workspace_set_attention_mode": (_i32, [_vp, _i32]),
@@ -463,3 +464,9 @@ def gelu_map(x_ptr, y_ptr, n, stream=None):
 def mfma_products(a_ptr, b_ptr, out_ptr, n_sets, stream=None):
     """Raw results of the attention kernels' exact-product MFMA (16 floats per lane per set of 64 pairs)."""
     _check(_lib.ae_debug_mfma_products(a_ptr, b_ptr, out_ptr, int(n_sets), stream))
+
+
+def set_attention_form(form):
+    """Exact-attention kernels to launch from now on: 0 by the batch (default),
+    1 tiled / register rows only, 2 the latency form only (a test hook)."""
+    _check(_lib.ae_debug_set_attention_form(int(form)))

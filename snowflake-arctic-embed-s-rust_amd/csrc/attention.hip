@@ -484,6 +484,190 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   }
 }
 
+// ---------------------------------------------------------------------------
+// Latency form, for batches of few tiles (a single sequence, the latency entry
+// points): one workgroup of 8 waves per (sequence, 16 queries, head), with the
+// arithmetic of attention_kernel<true> in the same order, laid out for a short
+// critical path rather than for throughput:
+//  * every global load (the Q operands, the K operands of the wave's key
+//    blocks, the head's V rows into LDS) is issued at the start;
+//  * scores: wave w takes the 16-key blocks w, w + 8, ...: MFMA products and
+//    in-order adds exactly as attention_kernel<true>'s phase 1;
+//  * exp and the in-order denominator as there;
+//  * PV on the VALU, one output (query, dim) per thread: p_t = e_t * inv and
+//    p_t * v_t,d rounded separately (the reference's `s[i] * inv`, then
+//    `p * v`), added in key order from LDS.
+// dynamic LDS: S[16][s_pitch] scores -> exps, then V[s_pitch - 4][32]
+// ---------------------------------------------------------------------------
+constexpr int kLatQ = 16;  // queries per workgroup
+
+__global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tiles_per_seq) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  __shared__ float s_maxw[8][kLatQ];
+  __shared__ float s_max[kLatQ], s_inv[kLatQ];
+  const int pitch = p.s_pitch, lmax = pitch - 4;
+  float* S = smem;                   // [kLatQ][pitch]
+  float* sV = smem + kLatQ * pitch;  // [lmax][32]
+  const int h = blockIdx.x % 12, bt = blockIdx.x / 12, b = bt / tiles_per_seq;
+  const int q0 = (bt - b * tiles_per_seq) * kLatQ;
+  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, lmax);
+  if (q0 >= L) return;  // workgroup-uniform
+  const int nq = min(kLatQ, L - q0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lg = lane >> 4;
+  const ExpTab tb = exp_tab_regs();
+  const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
+
+  // V rows (this head) to LDS: float4 f = tid + 512 i is key f / 8, dims 4 (f % 8) .. +3
+  constexpr int kVF = 8;  // float4s per thread at 512 keys
+  float4 vr[kVF];
+#pragma unroll
+  for (int i = 0; i < kVF; i++) {
+    const int f = tid + 512 * i;
+    if (f < 8 * L) vr[i] = *reinterpret_cast<const float4*>(qkv + (size_t)(f >> 3) * HQKV + 2 * H + (f & 7) * 4);
+  }
+  // operands of one row in the wide layout: f[4c + i] = dim 16c + 4lg + i
+  auto load_dims = [&](const float* row, float (&f)[8]) {
+    const float4* src = reinterpret_cast<const float4*>(row + 4 * lg);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const float4 v = src[4 * c];
+      f[4 * c] = v.x; f[4 * c + 1] = v.y; f[4 * c + 2] = v.z; f[4 * c + 3] = v.w;
+    }
+  };
+  float qf[8];  // query q0 + lr (rows past the segment clamped)
+  load_dims(qkv + (size_t)min(q0 + lr, L - 1) * HQKV, qf);
+  const int nkb = (L + 15) >> 4;  // <= 32: at most 4 blocks per wave
+  float kf[4][8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int kb = wave + 8 * j;
+    if (kb < nkb) load_dims(qkv + H + (size_t)min(16 * kb + lr, L - 1) * HQKV, kf[j]);
+  }
+#pragma unroll
+  for (int i = 0; i < kVF; i++) {
+    const int f = tid + 512 * i;
+    if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
+  }
+
+  // scores of query lr for keys 16kb + 4lg + i (dot32_f32 order) and the row max;
+  // keys >= L repeat key L - 1 (clamped rows) and cannot change the max
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int kb = wave + 8 * j;
+    if (kb < nkb) {  // wave-uniform
+      float acc[4];
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        v16f pr[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) pr[u] = mfma_products(kf[j][4 * c + u], qf[4 * c + u]);
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++)  // dims 16c + 4blk + u, in order
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              acc[i] = (c == 0 && blk == 0 && u == 0) ? pr[0][i] : acc[i] + pr[u][4 * blk + i];
+      }
+      float4 sc;
+      sc.x = acc[0] * kInvSqrtD;
+      sc.y = acc[1] * kInvSqrtD;
+      sc.z = acc[2] * kInvSqrtD;
+      sc.w = acc[3] * kInvSqrtD;
+      *reinterpret_cast<float4*>(&S[lr * pitch + 16 * kb + 4 * lg]) = sc;  // < round16(L) <= lmax
+      m = fmaxf(fmaxf(m, fmaxf(sc.x, sc.y)), fmaxf(sc.z, sc.w));
+    }
+  }
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, __shfl_xor(m, 32, 64));
+  if (lane < 16) s_maxw[wave][lane] = m;
+  __syncthreads();
+  if (tid < kLatQ) {
+    float mm = s_maxw[0][tid];
+#pragma unroll
+    for (int w = 1; w < 8; w++) mm = fmaxf(mm, s_maxw[w][tid]);
+    s_max[tid] = mm;
+  }
+  __syncthreads();
+
+  // e_t = expf(s_t - max) over the nq x ceil(L/4) float4s (as attention_kernel's phase 3)
+  {
+    const int cols4 = (L + 3) >> 2;
+    const float rcols = 1.0f / (float)cols4;  // q = floor((u + 0.5) / cols4): exact for u < 2^13
+    const int units = nq * cols4;
+    for (int u0 = 0; u0 < units; u0 += 1024) {  // uniform trip count (expf_libm needs all lanes)
+      float* e[2];
+      float4 v[2];
+      float mq[2];
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const int u = min(u0 + 512 * k + tid, units - 1);
+        const int q = (int)(((float)u + 0.5f) * rcols);
+        e[k] = &S[q * pitch + 4 * (u - q * cols4)];
+        v[k] = *reinterpret_cast<const float4*>(e[k]);
+        mq[k] = s_max[q];
+      }
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        v[k].x = expf_libm(v[k].x - mq[k], tb);
+        v[k].y = expf_libm(v[k].y - mq[k], tb);
+        v[k].z = expf_libm(v[k].z - mq[k], tb);
+        v[k].w = expf_libm(v[k].w - mq[k], tb);
+      }
+#pragma unroll
+      for (int k = 0; k < 2; k++)
+        if (u0 + 512 * k + tid < units) *reinterpret_cast<float4*>(e[k]) = v[k];
+    }
+  }
+  __syncthreads();
+  if (tid < kLatQ) {  // in-order denominator, one lane per query
+    float inv = 0.0f;
+    if (tid < nq) {
+      const float* e = &S[tid * pitch];
+      float sum = 0.0f;
+      int t = 0;
+      for (; t + 4 <= L; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(e + t);
+        sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+      }
+      for (; t < L; t++) sum += e[t];
+      inv = 1.0f / sum;
+    }
+    s_inv[tid] = inv;
+  }
+  __syncthreads();
+
+  // PV: thread (q, d) = (tid / 32, tid % 32)
+  const int q = tid >> 5, d = tid & 31;
+  float o = 0.0f;
+  if (q < nq) {  // uniform per half-wave
+    const float inv = s_inv[q];
+    const float* er = &S[q * pitch];
+    int t = 0;
+    for (; t + 4 <= L; t += 4) {
+      const float4 e4 = *reinterpret_cast<const float4*>(er + t);
+      o = o + (e4.x * inv) * sV[32 * t + d];
+      o = o + (e4.y * inv) * sV[32 * (t + 1) + d];
+      o = o + (e4.z * inv) * sV[32 * (t + 2) + d];
+      o = o + (e4.w * inv) * sV[32 * (t + 3) + d];
+    }
+    for (; t < L; t++) o = o + (er[t] * inv) * sV[32 * t + d];
+    p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = o;
+  }
+  if (p.rowmax) {
+    // max |ctx * inv_smooth| over the head's 32 dims (one half-wave; every value
+    // is a non-NaN >= +0 where fmaxf is the reference's scan), by atomicMax on
+    // the f32 bits
+    float a = q < nq ? nanless_max(0.0f, fabsf(o * p.smooth[h * 32 + d])) : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    if (d == 0 && q < nq) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
+  }
+}
+
 // Short rows (every sequence of the batch at most 16 * NKB <= 64 keys): one
 // workgroup per (sequence, head), one wave per 16 queries, the whole score row
 // in registers (NKB blocks of 16 keys, 4 scores per lane and block), no LDS tile
@@ -644,6 +828,7 @@ int attention_pitch(int max_len) {
 }
 
 __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p);
+__global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tiles_per_seq);
 
 // allow > 64 KiB of dynamic LDS for the tiled kernel on the current device; called
 // at engine open and by the stand-alone operator, never inside a stream capture
@@ -655,6 +840,9 @@ void init_attention_kernels() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(cls_attention_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sizeof(float) * 32 * 512));
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lat_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(sizeof(float) * (16 * (size_t)attention_pitch(512) + 32 * 512)));
 }
 
 // The wide variant (3 workgroups per CU by registers) is faster from rows of
@@ -668,9 +856,24 @@ void launch_attention_plan(const AttnArgs& p, int T, hipStream_t st) {
                      attention_max_tiles(p.B, T), reinterpret_cast<int4*>(p.plan));
 }
 
+// The latency form serves batches of at most this many 32-query tiles
+// (B * ceil(longest / 32)): below it the tiled kernel leaves most CUs idle and
+// its time is the critical path of one workgroup.
+constexpr int kLatMaxTiles = 16;
+static int g_attention_form = 0;  // 0 by the batch, 1 tiled / rows only, 2 latency form only
+void set_attention_form(int form) { g_attention_form = form; }
+
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
   if (T <= 0 || p.B <= 0) return;
   const int max_len = p.s_pitch - 4;  // round16 of the longest sequence
+  const bool lat = g_attention_form == 2 ||
+                   (g_attention_form == 0 && max_len > 64 && (size_t)p.B * ((max_len + 31) / 32) <= kLatMaxTiles);
+  if (lat) {
+    const int tps = (max_len + kLatQ - 1) / kLatQ;
+    const size_t lds = sizeof(float) * ((size_t)kLatQ * p.s_pitch + (size_t)max_len * 32);
+    hipLaunchKernelGGL(attention_lat_kernel, dim3(p.B * tps * 12), dim3(512), lds, st, p, tps);
+    return;
+  }
   if (max_len <= 32) {
     hipLaunchKernelGGL(attention_rows_kernel<2>, dim3(p.B * 12), dim3(256), 0, st, p);
     return;

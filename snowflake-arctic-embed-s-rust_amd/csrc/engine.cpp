@@ -1283,6 +1283,12 @@ int ae_debug_gelu_map(const float* x_dev, float* y_dev, size_t n, void* stream) 
 }
 
 // test hook: the attention kernels' exact-product MFMA
+int ae_debug_set_attention_form(int form) {
+  if (form < 0 || form > 2) return fail(AE_ERR_INVALID_ARG, "attention form must be 0, 1 or 2");
+  aek::set_attention_form(form);
+  return AE_OK;
+}
+
 int ae_debug_mfma_products(const float* a_dev, const float* b_dev, float* out_dev, int n_sets, void* stream) {
   if (!a_dev || !b_dev || !out_dev || n_sets < 0) return fail(AE_ERR_INVALID_ARG, "bad mfma_products arguments");
   aek::launch_mfma_products(a_dev, b_dev, out_dev, n_sets, as_stream(stream));

@@ -133,6 +133,9 @@ hipError_t noalloc_plan_scratch(int** plan);
 // (launch_attention_plan, which depends only on cu, B, T and s_pitch)
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
 void launch_attention_plan(const AttnArgs& p, int T, hipStream_t st);
+// exact-attention kernel choice for later launches: 0 by the batch, 1 tiled /
+// register rows only, 2 the latency form only (a test hook; same bits)
+void set_attention_form(int form);
 // Quantized attention (the reference's ArmSme backend): scratch for the int8 Q
 // and K of every token and head, their scales and the per-column |V| maximum.
 struct SmeArgs {

@@ -55,6 +55,24 @@ def test_c1_matches_golden_and_oracle(engine, ws, oracle_model):
     assert abs(np.linalg.norm(e.astype(np.float64)) - 1) < 1e-5
 
 
+@pytest.mark.parametrize("form", [1, 2], ids=["tiled", "latency_form"])
+def test_c1_through_each_attention_form(engine, oracle_model, form):
+    """C1 with the tiled attention kernel and with the latency form (which its shape
+    selects), each on a fresh workspace (graphs capture the kernels launched)."""
+    ids = c1_ids()
+    ae.set_attention_form(form)
+    try:
+        w = engine.workspace(512, 1)
+        e = engine.embed_tokens(w, ids)
+        e2 = engine.embed_tokens(w, ids)  # the captured graph's replay
+        w.close()
+    finally:
+        ae.set_attention_form(0)
+    ref = oracle_model.forward_cls(ids)
+    check_close(e, ref, "C1 form %d" % form)
+    assert np.array_equal(e, e2) and np.array_equal(e.astype(np.float32), ref.astype(np.float32))
+
+
 def test_ragged_batch_matches_oracle(engine, ws, oracle_model):
     gold = json.load(open(os.path.join(GOLDEN, "oracle_golden.json")))["ragged_seed3_n8_16_96"]
     seqs = ragged_batch(8, 16, 96, 3)

@@ -275,17 +275,30 @@ def test_gelu_bit_exact_over_float_sample(torch_gpu):
     assert np.array_equal(bits(y)[~nan], bits(ref)[~nan])
 
 
-# attention has four code paths, chosen by the batch's longest and mean lengths:
-# register-resident rows (longest <= 32, <= 64), else the tiled kernel with the
-# wide (mean > 48) or the narrow operand layout; these length sets reach each
+# exact attention has five code paths, chosen by the batch's shape: the latency
+# form (at most 16 tiles of 32 queries, longest > 64), register-resident rows
+# (longest <= 32, <= 64), else the tiled kernel with the wide (mean > 48) or the
+# narrow operand layout; these length sets reach each
 ATTN_LENS = {"tiled_wide": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
              "tiled_narrow": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 100],
              "rows64": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 64],
-             "rows32": [1, 2, 17, 31, 32, 3, 9, 16, 15, 8]}
+             "rows32": [1, 2, 17, 31, 32, 3, 9, 16, 15, 8],
+             "latency_128": [128],
+             "latency_ragged": [5, 97, 33],
+             "latency_512": [512]}
+
+
+@pytest.fixture(params=[0, 2], ids=["by_shape", "latency_form"])
+def attention_form(request, torch_gpu):
+    """Every exact-attention test runs with the kernel the batch's shape selects, and
+    again with the latency form forced onto the same batch."""
+    ae.set_attention_form(request.param)
+    yield request.param
+    ae.set_attention_form(0)
 
 
 @pytest.mark.parametrize("lens", list(ATTN_LENS.values()), ids=list(ATTN_LENS))
-def test_attention_bit_exact(torch_gpu, lens):
+def test_attention_bit_exact(torch_gpu, attention_form, lens):
     """Segment-bounded attention in the reference's scalar order: bit-exact."""
     torch = torch_gpu
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
@@ -294,6 +307,7 @@ def test_attention_bit_exact(torch_gpu, lens):
     qkv = rng.normal(0, 1.0, (T, 1152)).astype(f32)
     qkv_d, cu_d = dev(torch, qkv), dev(torch, cu)
     ctx_d = torch.zeros((T, 384), dtype=torch.float32, device="cuda")
+    print("attention form", attention_form, "lens", lens, flush=True)
     ae.attention_varlen(qkv_d.data_ptr(), cu_d.data_ptr(), len(lens), T, ctx_d.data_ptr())
     torch.cuda.synchronize()
     ref = orc.attention(qkv, cu)
@@ -353,9 +367,10 @@ def test_mfma_products_equal_rounded_products(torch_gpu):
     assert np.count_nonzero((ref != 0) & (np.abs(ref) < np.finfo(f32).tiny)) > 1000  # denormals were covered
 
 
-@pytest.mark.parametrize("lens", [[5, 40, 97, 300], [5, 40, 19, 33, 1, 90], [5, 40, 19, 33, 1], [5, 31, 19, 27, 1]],
-                         ids=["tiled_wide", "tiled_narrow", "rows64", "rows32"])
-def test_attention_bit_exact_extreme_magnitudes(torch_gpu, lens):
+@pytest.mark.parametrize("lens", [[5, 40, 97, 300], [5, 40, 19, 33, 1, 90], [5, 40, 19, 33, 1], [5, 31, 19, 27, 1],
+                                  [97, 5, 33]],
+                         ids=["tiled_wide", "tiled_narrow", "rows64", "rows32", "latency"])
+def test_attention_bit_exact_extreme_magnitudes(torch_gpu, attention_form, lens):
     """Scores and PV terms with denormal products, exact zeros and huge dynamic range."""
     torch = torch_gpu
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
