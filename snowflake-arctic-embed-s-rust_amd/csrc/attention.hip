@@ -494,9 +494,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
 //  * scores: wave w takes the 16-key blocks w, w + 8, ...: MFMA products and
 //    in-order adds exactly as attention_kernel<true>'s phase 1;
 //  * exp and the in-order denominator as there;
-//  * PV on the VALU, one output (query, dim) per thread: p_t = e_t * inv and
-//    p_t * v_t,d rounded separately (the reference's `s[i] * inv`, then
-//    `p * v`), added in key order from LDS.
+//  * p_t = e_t * inv in place (the reference's `s[i] * inv`), then PV on the
+//    VALU, one output (query, dim) per thread: p_t * v_t,d rounded, added in
+//    key order from LDS.
 // dynamic LDS: S[16][s_pitch] scores -> exps, then V[s_pitch - 4][32]
 // ---------------------------------------------------------------------------
 constexpr int kLatQ = 16;  // queries per workgroup
@@ -510,7 +510,8 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
   float* sV = smem + kLatQ * pitch;  // [lmax][32]
   const int h = blockIdx.x % 12, bt = blockIdx.x / 12, b = bt / tiles_per_seq;
   const int q0 = (bt - b * tiles_per_seq) * kLatQ;
-  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, lmax);
+  // a single segment whose bounds the host knows (p.len1 > 0): no cu_seqlens load
+  const int s0 = p.len1 > 0 ? 0 : p.cu[b], L = min(p.len1 > 0 ? p.len1 : p.cu[b + 1] - s0, lmax);
   if (q0 >= L) return;  // workgroup-uniform
   const int nq = min(kLatQ, L - q0);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -519,14 +520,6 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
   const ExpTab tb = exp_tab_regs();
   const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
 
-  // V rows (this head) to LDS: float4 f = tid + 512 i is key f / 8, dims 4 (f % 8) .. +3
-  constexpr int kVF = 8;  // float4s per thread at 512 keys
-  float4 vr[kVF];
-#pragma unroll
-  for (int i = 0; i < kVF; i++) {
-    const int f = tid + 512 * i;
-    if (f < 8 * L) vr[i] = *reinterpret_cast<const float4*>(qkv + (size_t)(f >> 3) * HQKV + 2 * H + (f & 7) * 4);
-  }
   // operands of one row in the wide layout: f[4c + i] = dim 16c + 4lg + i
   auto load_dims = [&](const float* row, float (&f)[8]) {
     const float4* src = reinterpret_cast<const float4*>(row + 4 * lg);
@@ -545,10 +538,14 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
     const int kb = wave + 8 * j;
     if (kb < nkb) load_dims(qkv + H + (size_t)min(16 * kb + lr, L - 1) * HQKV, kf[j]);
   }
+  // V rows (this head), issued after Q and K (the scores wait only for those):
+  // float4 f = tid + 512 i is key f / 8, dims 4 (f % 8) .. +3; to LDS after the scores
+  constexpr int kVF = 8;  // float4s per thread at 512 keys
+  float4 vr[kVF];
 #pragma unroll
   for (int i = 0; i < kVF; i++) {
     const int f = tid + 512 * i;
-    if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
+    if (f < 8 * L) vr[i] = *reinterpret_cast<const float4*>(qkv + (size_t)(f >> 3) * HQKV + 2 * H + (f & 7) * 4);
   }
 
   // scores of query lr for keys 16kb + 4lg + i (dot32_f32 order) and the row max;
@@ -584,6 +581,11 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
   m = fmaxf(m, __shfl_xor(m, 16, 64));
   m = fmaxf(m, __shfl_xor(m, 32, 64));
   if (lane < 16) s_maxw[wave][lane] = m;
+#pragma unroll
+  for (int i = 0; i < kVF; i++) {
+    const int f = tid + 512 * i;
+    if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
+  }
   __syncthreads();
   if (tid < kLatQ) {
     float mm = s_maxw[0][tid];
@@ -598,28 +600,17 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
     const int cols4 = (L + 3) >> 2;
     const float rcols = 1.0f / (float)cols4;  // q = floor((u + 0.5) / cols4): exact for u < 2^13
     const int units = nq * cols4;
-    for (int u0 = 0; u0 < units; u0 += 1024) {  // uniform trip count (expf_libm needs all lanes)
-      float* e[2];
-      float4 v[2];
-      float mq[2];
-#pragma unroll
-      for (int k = 0; k < 2; k++) {
-        const int u = min(u0 + 512 * k + tid, units - 1);
-        const int q = (int)(((float)u + 0.5f) * rcols);
-        e[k] = &S[q * pitch + 4 * (u - q * cols4)];
-        v[k] = *reinterpret_cast<const float4*>(e[k]);
-        mq[k] = s_max[q];
-      }
-#pragma unroll
-      for (int k = 0; k < 2; k++) {
-        v[k].x = expf_libm(v[k].x - mq[k], tb);
-        v[k].y = expf_libm(v[k].y - mq[k], tb);
-        v[k].z = expf_libm(v[k].z - mq[k], tb);
-        v[k].w = expf_libm(v[k].w - mq[k], tb);
-      }
-#pragma unroll
-      for (int k = 0; k < 2; k++)
-        if (u0 + 512 * k + tid < units) *reinterpret_cast<float4*>(e[k]) = v[k];
+    for (int u0 = 0; u0 < units; u0 += 512) {  // uniform trip count (expf_libm needs all lanes)
+      const int u = min(u0 + tid, units - 1);
+      const int q = (int)(((float)u + 0.5f) * rcols);
+      float* e = &S[q * pitch + 4 * (u - q * cols4)];
+      float4 v = *reinterpret_cast<const float4*>(e);
+      const float mq = s_max[q];
+      v.x = expf_libm(v.x - mq, tb);
+      v.y = expf_libm(v.y - mq, tb);
+      v.z = expf_libm(v.z - mq, tb);
+      v.w = expf_libm(v.w - mq, tb);
+      if (u0 + tid < units) *reinterpret_cast<float4*>(e) = v;
     }
   }
   __syncthreads();
@@ -628,33 +619,101 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
     if (tid < nq) {
       const float* e = &S[tid * pitch];
       float sum = 0.0f;
-      int t = 0;
-      for (; t + 4 <= L; t += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(e + t);
-        sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+      // batches of 16 keys, each read while the previous one is added (reads past
+      // the last full batch are clamped to it and not added)
+      const int nb = L >> 4;
+      float4 ea[4], eb[4];
+      auto ld = [&](int bi, float4 (&v)[4]) {
+        const float4* src = reinterpret_cast<const float4*>(e + 16 * min(bi, nb - 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = src[i];
+      };
+      auto add = [&](const float4 (&v)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sum += v[i].x; sum += v[i].y; sum += v[i].z; sum += v[i].w;
+        }
+      };
+      if (nb > 0) {
+        ld(0, ea);
+        int bi = 0;
+        for (; bi + 2 <= nb; bi += 2) {
+          ld(bi + 1, eb);
+          __builtin_amdgcn_sched_barrier(0);
+          add(ea);
+          __builtin_amdgcn_sched_barrier(0);
+          ld(bi + 2, ea);
+          __builtin_amdgcn_sched_barrier(0);
+          add(eb);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (bi < nb) add(ea);
       }
-      for (; t < L; t++) sum += e[t];
+      for (int t = 16 * nb; t < L; t++) sum += e[t];
       inv = 1.0f / sum;
     }
     s_inv[tid] = inv;
   }
   __syncthreads();
+  // p_t = e_t * inv in place (the reference's normalization), one float4 per thread and step
+  {
+    const int cols4 = (L + 3) >> 2;
+    const float rcols = 1.0f / (float)cols4;
+    const int units = nq * cols4;
+    for (int u = tid; u < units; u += 512) {
+      const int q = (int)(((float)u + 0.5f) * rcols);
+      float4* e = reinterpret_cast<float4*>(&S[q * pitch + 4 * (u - q * cols4)]);
+      const float inv = s_inv[q];
+      float4 v = *e;
+      v.x = v.x * inv; v.y = v.y * inv; v.z = v.z * inv; v.w = v.w * inv;
+      *e = v;
+    }
+  }
+  __syncthreads();
 
-  // PV: thread (q, d) = (tid / 32, tid % 32)
+  // PV: thread (q, d) = (tid / 32, tid % 32), p_t * v_t,d added in key order
   const int q = tid >> 5, d = tid & 31;
   float o = 0.0f;
   if (q < nq) {  // uniform per half-wave
-    const float inv = s_inv[q];
-    const float* er = &S[q * pitch];
-    int t = 0;
-    for (; t + 4 <= L; t += 4) {
-      const float4 e4 = *reinterpret_cast<const float4*>(er + t);
-      o = o + (e4.x * inv) * sV[32 * t + d];
-      o = o + (e4.y * inv) * sV[32 * (t + 1) + d];
-      o = o + (e4.z * inv) * sV[32 * (t + 2) + d];
-      o = o + (e4.w * inv) * sV[32 * (t + 3) + d];
+    const float* pr = &S[q * pitch];
+    // batches of 8 keys: the next batch's LDS reads go out before this batch's
+    // chain of adds (reads past the last full batch are clamped to it, not used)
+    const int nb = L >> 3;
+    float4 pa[2], pb[2];
+    float va[8], vb[8];
+    auto ld = [&](int bi, float4 (&pp)[2], float (&v)[8]) {
+      const int t0 = 8 * min(bi, nb - 1);
+      pp[0] = *reinterpret_cast<const float4*>(pr + t0);
+      pp[1] = *reinterpret_cast<const float4*>(pr + t0 + 4);
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = sV[32 * (t0 + k) + d];
+    };
+    auto add = [&](const float4 (&pp)[2], const float (&v)[8]) {
+      o = o + pp[0].x * v[0];
+      o = o + pp[0].y * v[1];
+      o = o + pp[0].z * v[2];
+      o = o + pp[0].w * v[3];
+      o = o + pp[1].x * v[4];
+      o = o + pp[1].y * v[5];
+      o = o + pp[1].z * v[6];
+      o = o + pp[1].w * v[7];
+    };
+    if (nb > 0) {
+      ld(0, pa, va);
+      int bi = 0;
+      for (; bi + 2 <= nb; bi += 2) {
+        ld(bi + 1, pb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        add(pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(bi + 2, pa, va);
+        __builtin_amdgcn_sched_barrier(0);
+        add(pb, vb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (bi < nb) add(pa, va);
     }
-    for (; t < L; t++) o = o + (er[t] * inv) * sV[32 * t + d];
+    for (int t = 8 * nb; t < L; t++) o = o + pr[t] * sV[32 * t + d];
     p.ctx[(size_t)(s0 + q0 + q) * H + h * 32 + d] = o;
   }
   if (p.rowmax) {

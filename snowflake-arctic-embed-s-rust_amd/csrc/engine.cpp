@@ -407,9 +407,10 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   sme_args.per_seq = 1;
   // Few rows (gemm_small_path): every LayerNorm runs in the prologue of the GEMM
   // that consumes it (QKV, FFN-up, the layer-11 K/V), whose column-tile-0
-  // workgroups also store its outputs, so the attn_out / FFN-down GEMMs spread
-  // their weight columns over twice the workgroups (no whole-row epilogue).
-  // The row-absmax targets of a layer (attention -> rowmax_ctx, GELU -> rowmax_g)
+  // workgroups also store its outputs; the attention output GEMM runs inside the
+  // FFN-up kernel, in front of LN1 (each workgroup for its 16 rows), and LN1's
+  // output (the FFN-down residual, updated in place) lives in tmp.  The
+  // row-absmax targets of a layer (attention -> rowmax_ctx, GELU -> rowmax_g)
   // are reset by the LayerNorm that precedes the layer.
   const bool small = gemm_small_path(T);
   const float* ln2_w = nullptr;  // small: the previous layer's LN2, applied by the next QKV prologue
@@ -432,6 +433,8 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     {
       KernelTimer kt(ws, st, AE_KERNEL_ATTENTION);
       AttnArgs a{ws->qkv, cu, B, ws->attn_plan, ws->ctx, D.attn_out.inv_smooth, ws->rowmax_ctx, s_pitch};
+      // one sequence: the device check holds cu_seqlens to {0, T} (else the error word is set)
+      if (B == 1) a.len1 = T;
       if (sme) {
         launch_attention_sme(a, sme_args, T, st, /*plan=*/l == 0);
         launch_attention_short(a, st);
@@ -440,22 +443,20 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       }
     }
     if (small) {
-      {
-        KernelTimer kt(ws, st, AE_KERNEL_GEMM_ATTN_OUT);
-        gemm(D.attn_out, T, ws->ctx, kAF32QSmooth, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
-             kEpiF32, nullptr, nullptr);
-      }
-      {
+      {  // attention output GEMM + LN1 + FFN-up/GELU in one kernel; LN1's output goes to tmp
         KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
-        launch_gemm_ln_prologue(gemm_args(D.ffn_inter, T, ws->tmp, nullptr, nullptr, nullptr, nullptr, ws->g,
-                                          D.ffn_out.inv_smooth, ws->rowmax_g),
-                                ln_args(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr,
-                                        nullptr, nullptr, T),
-                                kEpiGelu, st);
+        const PreArgs pre{ws->ctx, ws->rowmax_ctx, D.attn_out.inv_smooth, D.attn_out.w, D.attn_out.w_scale,
+                          D.attn_out.bias, ws->hidden};
+        launch_gemm_pre_ln(gemm_args(D.ffn_inter, T, nullptr, nullptr, nullptr, nullptr, nullptr, ws->g,
+                                     D.ffn_out.inv_smooth, ws->rowmax_g),
+                           pre,
+                           ln_args(nullptr, ws->tmp, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr, nullptr,
+                                   nullptr, T),
+                           kEpiGelu, st);
       }
-      {
+      {  // residual LN1(h) in tmp, written in place
         KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_DOWN);
-        gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->hidden, ws->tmp, kEpiF32, nullptr,
+        gemm(D.ffn_out, T, ws->g, kAF32Q, nullptr, ws->rowmax_g, nullptr, ws->tmp, ws->tmp, kEpiF32, nullptr,
              nullptr);
       }
       ln2_w = D.ln2_w;
@@ -532,15 +533,16 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   launch_cls(c, 0, st);
   gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
   launch_cls(c, 1, st);
-  if (small_tail) {  // LN1 in the FFN-up prologue (rowmax_g_c reset by the [CLS] gather)
-    gemm(D.attn_out, B, ws->ctx_c, kAF32QSmooth, nullptr, ws->rowmax_ctx_c, D.attn_out.inv_smooth, ws->hidden_c,
-         ws->tmp_c, kEpiF32, nullptr, nullptr);
-    launch_gemm_ln_prologue(gemm_args(D.ffn_inter, B, ws->tmp_c, nullptr, nullptr, nullptr, nullptr, ws->g_c,
-                                      D.ffn_out.inv_smooth, ws->rowmax_g_c),
-                            ln_args(ws->tmp_c, ws->hidden_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr, nullptr,
-                                    nullptr, B),
-                            kEpiGelu, st);
-    gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->hidden_c, ws->tmp_c, kEpiF32, nullptr,
+  if (small_tail) {  // attention output + LN1 + FFN-up in one kernel (rowmax_g_c reset by the [CLS] gather)
+    const PreArgs pre{ws->ctx_c, ws->rowmax_ctx_c, D.attn_out.inv_smooth, D.attn_out.w, D.attn_out.w_scale,
+                      D.attn_out.bias, ws->hidden_c};
+    launch_gemm_pre_ln(gemm_args(D.ffn_inter, B, nullptr, nullptr, nullptr, nullptr, nullptr, ws->g_c,
+                                 D.ffn_out.inv_smooth, ws->rowmax_g_c),
+                       pre,
+                       ln_args(nullptr, ws->tmp_c, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, nullptr, nullptr, nullptr,
+                               B),
+                       kEpiGelu, st);
+    gemm(D.ffn_out, B, ws->g_c, kAF32Q, nullptr, ws->rowmax_g_c, nullptr, ws->tmp_c, ws->tmp_c, kEpiF32, nullptr,
          nullptr);
     launch_final_ln_l2(B, ws->tmp_c, D.ln2_w, D.ln2_b, out, st);
   } else {

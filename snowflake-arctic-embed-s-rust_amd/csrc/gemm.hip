@@ -278,15 +278,16 @@ constexpr int kLnPitchS = 388;                // LDS floats per row of the fused
 constexpr int kEPitchS = 52;                  // LDS words per row of a wave's epilogue staging tile
 
 template <int AM, int EM, bool LN, int KS>
-__global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) {
+__global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, PreArgs pre) {
   constexpr int WAVES = 8, NW = 48, kThreads = 512;
   constexpr int CG = WAVES / KS, kBN = CG * NW, kCB = NW / 16, kF4 = NW / 4;
   constexpr int RPW = 16 / KS, kPos = RPW * kF4, kEk = (kPos + 63) / 64;  // epilogue rows / float4s per wave
-  constexpr int kRing = 8;
+  constexpr int kRing = KS == 1 ? 6 : 3;  // B ring depth (K steps in flight per wave)
+  constexpr bool kLnIn = AM == kALn || AM == kAPreLn;  // a LayerNorm in front of the GEMM
   static_assert(KS == 1 || KS == 2 || KS == 8, "K splits");
   static_assert(!LN || (KS == 1 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
-  static_assert(AM != kALn || !LN, "LayerNorm prologue or epilogue");
-  constexpr bool kLnTile = LN || AM == kALn;  // an f32 row tile for a LayerNorm
+  static_assert(!kLnIn || !LN, "LayerNorm prologue or epilogue");
+  constexpr bool kLnTile = LN || kLnIn;  // an f32 row tile for a LayerNorm
   __shared__ __attribute__((aligned(16))) int8_t sA[16 * kSmallPitch];
   __shared__ __attribute__((aligned(16))) int sE[WAVES][16 * kEPitchS];
   static_assert(!kLnTile || sizeof(sE) >= 16 * kLnPitchS * sizeof(float), "LN squares reuse the staging tile");
@@ -294,6 +295,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) 
   __shared__ __attribute__((aligned(16))) float sEpSa[16], sEpWs[kBN], sEpB[kBN];
   __shared__ __attribute__((aligned(16))) float sLn[kLnTile ? 16 * kLnPitchS : 4];
   __shared__ float s_stat[2][16];
+  __shared__ float s_pre_sa[16];  // kAPreLn: the first GEMM's row scales
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fk = (lane >> 4) * 16;
   const int mt = (p.M + 15) >> 4;
@@ -317,10 +319,39 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) 
   v4i qa[kChunks];                                          // kAI8
   float4 xa[kChunks][4];                                    // f32 A
   float a_inv[kChunks];
-  if constexpr (AM == kALn) {
-    const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)min(lrow, p.M - 1) * 384;
+  // kAPreLn: the first GEMM's A chunk (thread t < 384: row t / 24, columns
+  // 16 (t % 24) .. +15) and row max, all six K steps of its weight fragments for
+  // this wave's 48 columns, and the epilogue operands of its 3 float4 positions
+  float4 pa[4], pres[3], pws[3], pbias[3];
+  float pa_max = 1.0f;
+  v4i pring[6][kCB];
+  if constexpr (AM == kAPreLn) {
+    if (tid < 384) {
+      const int row = min(m0 + tid / 24, p.M - 1);
 #pragma unroll
-    for (int i = 0; i < 3; i++) xv[i] = *reinterpret_cast<const float4*>(xr + (sub + 32 * i) * 4);
+      for (int k = 0; k < 4; k++) pa[k] = reinterpret_cast<const float4*>(pre.A + (size_t)row * 384 + (tid % 24) * 16)[k];
+      pa_max = __uint_as_float(pre.a_rowmax[row]);
+    }
+    const int8_t* pw = pre.w + (size_t)lane * 16;
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++)
+#pragma unroll
+      for (int j = 0; j < kCB; j++)
+        pring[kt][j] = *reinterpret_cast<const v4i*>(pw + ((size_t)kt * 24 + wave * kCB + j) * 1024);
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+      const int e = lane + 64 * k, er = e / kF4, col = wave * NW + (e % kF4) * 4;
+      pres[k] = *reinterpret_cast<const float4*>(pre.res + (size_t)min(m0 + er, p.M - 1) * 384 + col);
+      pws[k] = *reinterpret_cast<const float4*>(pre.w_scale + col);
+      pbias[k] = *reinterpret_cast<const float4*>(pre.bias + col);
+    }
+  }
+  if constexpr (kLnIn) {
+    if constexpr (AM == kALn) {
+      const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)min(lrow, p.M - 1) * 384;
+#pragma unroll
+      for (int i = 0; i < 3; i++) xv[i] = *reinterpret_cast<const float4*>(xr + (sub + 32 * i) * 4);
+    }
 #pragma unroll
     for (int i = 0; i < 3; i++) {
       const int c = (sub + 32 * i) * 4;
@@ -360,15 +391,17 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) 
     for (int j = 0; j < kCB; j++)
       dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)(kb0 + kt) * NB + cb0 + j) * 1024);
   };
+  if constexpr (AM != kAPreLn) {  // (kAPreLn: after the first GEMM)
 #pragma unroll
-  for (int u = 0; u < kRing; u++)
-    if (u < KT) bload(u, bring[u]);
+    for (int u = 0; u < kRing; u++)
+      if (u < KT) bload(u, bring[u]);
+  }
   // epilogue operands: row scales, w_scale and bias of the workgroup's columns
   float4 ep_reg = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (tid < 16) {
     const int r = min(m0 + tid, p.M - 1);
     if (AM == kAI8) ep_reg.x = p.a_scale[r];
-    else if (AM != kALn) ep_reg.x = __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
+    else if (!kLnIn) ep_reg.x = __uint_as_float(p.a_rowmax[r]) / 127.0f;  // scale = max_abs / 127.0
   } else if (tid < 16 + kBN / 4) {
     ep_reg = reinterpret_cast<const float4*>(p.w_scale + n0)[tid - 16];
   } else if (tid < 16 + kBN / 2) {
@@ -393,16 +426,73 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) 
   }
 
   // the A tile into LDS: int8 A as loaded, f32 A quantized as astore does above,
-  // kALn through the LayerNorm
-  if constexpr (AM == kALn) {
+  // kALn through the LayerNorm; kAPreLn: the first GEMM's rows, then the LayerNorm
+  if constexpr (AM == kAPreLn) {
+    // its A tile (quantized as kAF32QSmooth) and row scales
+    if (tid < 384) {
+      const int r = tid / 24, kc = (tid % 24) * 16;
+      const float inv = 127.0f / pa_max;  // inv_scale = 127.0 / max_abs
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float4 sm = reinterpret_cast<const float4*>(pre.a_smooth + kc)[k];
+        const float4 v = make_float4(pa[k].x * sm.x, pa[k].y * sm.y, pa[k].z * sm.z, pa[k].w * sm.w);
+        w[k] = pack4(qround(v.x * inv), qround(v.y * inv), qround(v.z * inv), qround(v.w * inv));
+      }
+      *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + kc]) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+      if (tid % 24 == 0) s_pre_sa[r] = pa_max / 127.0f;  // scale = max_abs / 127.0
+    }
+    __syncthreads();
+    // its K loop: this wave's 48 columns, all six K steps
+    v4i acc1[kCB];
+#pragma unroll
+    for (int j = 0; j < kCB; j++) acc1[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++) {
+      const v4i af = *reinterpret_cast<const v4i*>(&sA[fr * kSmallPitch + kt * 64 + fk]);
+#pragma unroll
+      for (int j = 0; j < kCB; j++) acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, pring[kt][j], acc1[j], 0, 0, 0);
+    }
+    // the second GEMM's B ring, whose latency hides behind the LayerNorm
+#pragma unroll
+    for (int u = 0; u < kRing; u++)
+      if (u < KT) bload(u, bring[u]);
+    // its epilogue, through this wave's staging tile, into the LayerNorm's row tile
+    int* E1 = sE[wave];
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) E1[((lane >> 4) * 4 + r) * kEPitchS + j * 16 + fr] = acc1[j][r];
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+      const int e = lane + 64 * k, er = e / kF4, c4 = e % kF4;
+      const int4 a4 = *reinterpret_cast<const int4*>(&E1[er * kEPitchS + c4 * 4]);
+      const float sa = s_pre_sa[er];
+      float4 b4 = pbias[k];
+      b4.x = b4.x + pres[k].x; b4.y = b4.y + pres[k].y; b4.z = b4.z + pres[k].z; b4.w = b4.w + pres[k].w;
+      float4 v;
+      v.x = fmaf((float)a4.x, sa * pws[k].x, b4.x);
+      v.y = fmaf((float)a4.y, sa * pws[k].y, b4.y);
+      v.z = fmaf((float)a4.z, sa * pws[k].z, b4.z);
+      v.w = fmaf((float)a4.w, sa * pws[k].w, b4.w);
+      *reinterpret_cast<float4*>(&sLn[er * kLnPitchS + wave * NW + c4 * 4]) = v;
+    }
+    __syncthreads();  // sA is free again; the rows are in sLn
+#pragma unroll
+    for (int i = 0; i < 3; i++) xv[i] = *reinterpret_cast<const float4*>(&sLn[rr * kLnPitchS + (sub + 32 * i) * 4]);
+  }
+  if constexpr (kLnIn) {
     // LayerNorm + SmoothQuant of the 16 rows (layernorm_smooth_quantize_row_scalar,
     // reference src/simd_math.rs:208-247, as ln_quant_kernel computes it): one
     // lane per row takes the in-order sums, 32 threads per row the rest; the
     // int8 result is the A tile and its scale the epilogue's row scale.
     const bool writer = n0 == 0 && lrow < p.M;
+    if constexpr (AM == kALn) {
 #pragma unroll
-    for (int i = 0; i < 3; i++) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + (sub + 32 * i) * 4]) = xv[i];
-    __syncthreads();
+      for (int i = 0; i < 3; i++) *reinterpret_cast<float4*>(&sLn[rr * kLnPitchS + (sub + 32 * i) * 4]) = xv[i];
+      __syncthreads();
+    }
     if (tid < 16) s_stat[0][tid] = lds_row_sum(&sLn[tid * kLnPitchS], [](float x) { return x; }) / 384.0f;
     __syncthreads();
     const float mean = s_stat[0][rr];
@@ -483,7 +573,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln) 
     }
   }
   if (tid < 16) {
-    if (AM != kALn) sEpSa[tid] = ep_reg.x;
+    if (!kLnIn) sEpSa[tid] = ep_reg.x;
   } else if (tid < 16 + kBN / 4) {
     reinterpret_cast<float4*>(sEpWs)[tid - 16] = ep_reg;
   } else if (tid < 16 + kBN / 2) {
@@ -652,13 +742,13 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
   const int mt16 = (p.M + 15) / 16;
   if (small_gemm(p)) {
     if (ln) {
-      hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, true, 1>), dim3(mt16), dim3(512), 0, st, p, *ln);
+      hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, true, 1>), dim3(mt16), dim3(512), 0, st, p, *ln, PreArgs{});
     } else if (EM == kEpiF32 && p.K >= kSplitMinK && p.K % 512 == 0) {
       hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, false, 8>), dim3(mt16 * (p.N / 48)), dim3(512), 0, st, p,
-                         LnArgs{});
+                         LnArgs{}, PreArgs{});
     } else {
       hipLaunchKernelGGL((gemm_small_kernel<AM, EM, false, 2>), dim3(mt16 * (p.N / 192)), dim3(512), 0, st, p,
-                         LnArgs{});
+                         LnArgs{}, PreArgs{});
     }
     return;
   }
@@ -674,8 +764,19 @@ bool gemm_small_path(int m) { return m > 0 && m <= kSmallM; }
 void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st) {
   if (p.M <= 0 || p.M > kSmallM || p.K != 384) return;
   const dim3 grid(((p.M + 15) / 16) * (p.N / 192));
-  if (emode == kEpiGelu) hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, false, 2>), grid, dim3(512), 0, st, p, ln);
-  else hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, false, 2>), grid, dim3(512), 0, st, p, ln);
+  if (emode == kEpiGelu)
+    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, false, 2>), grid, dim3(512), 0, st, p, ln, PreArgs{});
+  else
+    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, false, 2>), grid, dim3(512), 0, st, p, ln, PreArgs{});
+}
+
+void launch_gemm_pre_ln(const GemmArgs& p, const PreArgs& pre, const LnArgs& ln, int emode, hipStream_t st) {
+  if (p.M <= 0 || p.M > kSmallM || p.K != 384) return;
+  const dim3 grid(((p.M + 15) / 16) * (p.N / 192));
+  if (emode == kEpiGelu)
+    hipLaunchKernelGGL((gemm_small_kernel<kAPreLn, kEpiGelu, false, 2>), grid, dim3(512), 0, st, p, ln, pre);
+  else
+    hipLaunchKernelGGL((gemm_small_kernel<kAPreLn, kEpiF32, false, 2>), grid, dim3(512), 0, st, p, ln, pre);
 }
 
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {

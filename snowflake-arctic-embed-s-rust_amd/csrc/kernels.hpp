@@ -12,6 +12,7 @@ constexpr int kAI8 = 0;          // int8 rows + per-row scale
 constexpr int kAF32Q = 1;        // f32 rows quantized on load: q = round(x * (127/max))
 constexpr int kAF32QSmooth = 2;  // f32 rows quantized on load: q = round((x * s_k) * (127/max))
 constexpr int kALn = 3;          // f32 rows (K = 384) put through the LayerNorm + SmoothQuant of an LnArgs
+constexpr int kAPreLn = 4;       // kALn whose f32 rows come from an N = 384 GEMM of a PreArgs in the same kernel
                                  // first (launch_gemm_ln_prologue, few rows only)
 // GEMM epilogues
 constexpr int kEpiF32 = 0;   // out = fma(f32(acc), sa*ws, bias (+res))
@@ -99,6 +100,22 @@ bool gemm_fuses_ln(const GemmArgs& p);
 // LayerNorm's outputs (ln.dst, and ln.q / ln.scale / ln.rowmax_init* when set).
 // ln.dst must not alias p.A.
 void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st);
+// The GEMM in front of such a LayerNorm (kAPreLn): x = fma(f32(q(A) . W^T), sa * ws,
+// bias + res) with A [M,384] f32 quantized on load as kAF32QSmooth does (sa =
+// max_abs / 127 from a_rowmax), W [384,384] pre-swizzled.
+struct PreArgs {
+  const float* A;
+  const uint32_t* a_rowmax;
+  const float* a_smooth;
+  const int8_t* w;
+  const float* w_scale;
+  const float* bias;
+  const float* res;
+};
+// Few rows: launch_gemm_ln_prologue with the LayerNorm's input rows computed in
+// every workgroup by `pre` (the attention-output GEMM in front of LN1, then the
+// FFN-up GEMM): one kernel instead of two.  ln.dst must not alias pre.res or pre.A.
+void launch_gemm_pre_ln(const GemmArgs& p, const PreArgs& pre, const LnArgs& ln, int emode, hipStream_t st);
 // whether launch_gemm takes the few-rows kernels for m rows (and the prologue form applies)
 bool gemm_small_path(int m);
 
@@ -115,6 +132,7 @@ struct AttnArgs {
   uint32_t* rowmax;        // [T] or null
   int s_pitch;             // score row pitch: attention_pitch(max sequence length)
   int skip_from = 0;       // attention_rows_kernel: segments of at least this many tokens are left out (0: none)
+  int len1 = 0;            // B == 1 and cu_seqlens = {0, len1} known on the host: the latency form skips its load
 };
 int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
