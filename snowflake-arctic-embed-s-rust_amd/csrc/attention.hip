@@ -994,36 +994,41 @@ void launch_attention_short(const AttnArgs& p, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // Layer-11 [CLS] pruning (reference src/model.rs:770-913)
 // ---------------------------------------------------------------------------
-// gather the B [CLS] rows (act_q, act_scale, hidden) into compact buffers
-__global__ __launch_bounds__(128) void gather_cls_kernel(ClsArgs p) {
-  const int b = blockIdx.x, t = threadIdx.x;
-  const int src = p.cu[b];
-  if (t < 96) {
-    reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[t] = reinterpret_cast<const float4*>(p.hidden + (size_t)src * H)[t];
-    reinterpret_cast<uint32_t*>(p.act_q_c + (size_t)b * H)[t] = reinterpret_cast<const uint32_t*>(p.act_q + (size_t)src * H)[t];
-  }
-  if (t == 0) {
-    p.act_scale_c[b] = p.act_scale[src];
-    p.rowmax_init[b] = __float_as_uint(1e-8f);
-    if (p.rowmax_init2) p.rowmax_init2[b] = __float_as_uint(1e-8f);
-  }
-}
-
 // one workgroup (4 waves) per (sequence, head): the [CLS] query attends to its
 // segment with the same exact scalar order as attention_kernel
-// (src/model.rs:814-843).  Every global load is issued at the start: the K rows
-// of the thread's keys (tid, tid + 256) and the segment's V rows, which go to LDS
-// ([key][32], dynamic, p.max_len keys) for the in-order PV sums.  Keys past
-// p.max_len (<= 512) are not attended (the embedding kernel reports such
-// sequences through the workspace's error word).
+// (src/model.rs:814-843).  Every global load is issued at the start: the [CLS]
+// row's int8 activations and the head's q_only weight fragments, the K rows of
+// the thread's keys (tid, tid + 256) and the segment's V rows, which go to LDS
+// ([key][32], dynamic, p.max_len keys) for the in-order PV sums.  Wave 0 forms
+// the head's 32 q values as the q_only GEMM does for that row (int8 MFMA with
+// the [CLS] row as row 0 of the A tile, then fma(f32(acc), sa * ws, bias)).
+// Keys past p.max_len (<= 512) are not attended (the embedding kernel reports
+// such sequences through the workspace's error word).
 __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   extern __shared__ __attribute__((aligned(16))) float sV[];  // [L][32]
   __shared__ __attribute__((aligned(16))) float S[512];
+  __shared__ __attribute__((aligned(16))) float sQ[32];
   __shared__ float s_m[4];
   __shared__ float s_inv;
   const int b = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, p.max_len);
   const ExpTab tb = exp_tab_regs();
+  // q_only for the [CLS] row and this head's 32 columns: A fragment (row 0 only,
+  // K steps 0..5) and the two 16-column weight blocks (fragment order of
+  // swizzle_weights: [K/64][N/16][64 lanes][16 bytes])
+  v4i qa[6], qb[6][2];
+  if (wave == 0) {
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++) {
+      qa[kt] = (lane & 15) == 0 ? *reinterpret_cast<const v4i*>(p.act_q + (size_t)s0 * H + kt * 64 + (lane >> 4) * 16)
+                                : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        qb[kt][j] = *reinterpret_cast<const v4i*>(p.wq + (((size_t)kt * (H / 16) + 2 * h + j) * 64 + lane) * 16);
+    }
+  }
+  if (h == 0 && tid < 96)  // gather the [CLS] row of hidden (the tail's residual)
+    reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[tid] = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[tid];
   // V: float4 f = tid + 256 i is key f / 8, dims 4 (f % 8) .. +3
   constexpr int kVF = 512 * 8 / 256;
   float4 vr[kVF];
@@ -1041,16 +1046,32 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
       for (int e = 0; e < 8; e++) kr[u][e] = *reinterpret_cast<const float4*>(p.kv + (size_t)(s0 + j) * 2 * H + h * 32 + 4 * e);
     }
   }
-  float q[32];
+  if (wave == 0) {
+    v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
 #pragma unroll
-  for (int d = 0; d < 32; d += 4) {
-    const float4 v = *reinterpret_cast<const float4*>(p.q_c + (size_t)b * H + h * 32 + d);
-    q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
+    for (int kt = 0; kt < 6; kt++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[kt], qb[kt][j], acc[j], 0, 0, 0);
+    if (lane < 16) {  // row 0 of the result: lane l holds columns 16 j + l, register 0
+      const float sa = p.act_scale[s0];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int col = h * 32 + 16 * j + lane;
+        sQ[16 * j + lane] = fmaf((float)acc[j][0], sa * p.wq_scale[col], p.wq_bias[col]);
+      }
+    }
   }
 #pragma unroll
   for (int i = 0; i < kVF; i++) {
     const int f = tid + 256 * i;
     if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
+  }
+  __syncthreads();
+  float q[32];
+#pragma unroll
+  for (int d = 0; d < 32; d += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(&sQ[d]);
+    q[d] = v.x; q[d + 1] = v.y; q[d + 2] = v.z; q[d + 3] = v.w;
   }
   // scores (dot32_f32 order) and their max
   float m = -INFINITY;
@@ -1122,10 +1143,8 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   }
 }
 
-void launch_cls(const ClsArgs& p, int stage, hipStream_t st) {
-  if (stage == 0) hipLaunchKernelGGL(gather_cls_kernel, dim3(p.B), dim3(128), 0, st, p);
-  else if (stage == 1)
-    hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), sizeof(float) * 32 * (size_t)p.max_len, st, p);
+void launch_cls(const ClsArgs& p, hipStream_t st) {
+  hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), sizeof(float) * 32 * (size_t)p.max_len, st, p);
 }
 
 }  // namespace aek

@@ -151,7 +151,7 @@ struct ae_workspace {
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
   uint32_t *rowmax_ctx = nullptr, *rowmax_g = nullptr;
-  float *hidden_c = nullptr, *tmp_c = nullptr, *q_c = nullptr, *ctx_c = nullptr, *g_c = nullptr, *out_c = nullptr;
+  float *hidden_c = nullptr, *tmp_c = nullptr, *ctx_c = nullptr, *g_c = nullptr, *out_c = nullptr;
   int8_t* act_q_c = nullptr;
   float* act_scale_c = nullptr;
   uint32_t *rowmax_ctx_c = nullptr, *rowmax_g_c = nullptr;
@@ -392,6 +392,9 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
     p.scale = ws->act_scale;
     p.rowmax_init = ws->rowmax_ctx;
     p.rowmax_init2 = gemm_small_path(T) ? ws->rowmax_g : nullptr;
+    p.rowmax_c = ws->rowmax_ctx_c;  // the layer-11 [CLS] rows' targets (row b < B)
+    p.rowmax_c2 = ws->rowmax_g_c;
+    p.n_c = B;
     p.max_len = max_len;
     p.err = ws->err;
     launch_ln_quant(p, kLnSrcEmb, st);
@@ -520,20 +523,16 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   c.act_q = ws->act_q;
   c.act_scale = ws->act_scale;
   c.hidden_c = ws->hidden_c;
-  c.act_q_c = ws->act_q_c;
-  c.act_scale_c = ws->act_scale_c;
-  c.rowmax_init = ws->rowmax_ctx_c;
-  c.rowmax_init2 = ws->rowmax_g_c;
-  c.q_c = ws->q_c;
+  c.wq = D.q_only.w;
+  c.wq_scale = D.q_only.w_scale;
+  c.wq_bias = D.q_only.bias;
   c.kv = kv;
   c.ctx_c = ws->ctx_c;
   c.smooth = D.attn_out.inv_smooth;
-  c.rowmax_ctx_c = ws->rowmax_ctx_c;
+  c.rowmax_ctx_c = ws->rowmax_ctx_c;  // reset by the embedding kernel
   c.max_len = std::min(max_len, ae::kMaxPos);
-  launch_cls(c, 0, st);
-  gemm(D.q_only, B, ws->act_q_c, kAI8, ws->act_scale_c, nullptr, nullptr, nullptr, ws->q_c, kEpiF32, nullptr, nullptr);
-  launch_cls(c, 1, st);
-  if (small_tail) {  // attention output + LN1 + FFN-up in one kernel (rowmax_g_c reset by the [CLS] gather)
+  launch_cls(c, st);
+  if (small_tail) {  // attention output + LN1 + FFN-up in one kernel (rowmax_g_c reset by the embedding kernel)
     const PreArgs pre{ws->ctx_c, ws->rowmax_ctx_c, D.attn_out.inv_smooth, D.attn_out.w, D.attn_out.w_scale,
                       D.attn_out.bias, ws->hidden_c};
     launch_gemm_pre_ln(gemm_args(D.ffn_inter, B, nullptr, nullptr, nullptr, nullptr, nullptr, ws->g_c,
@@ -775,7 +774,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
       (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
       (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
       (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
-      (rc = A(&ws->hidden_c, B * 384)) || (rc = A(&ws->tmp_c, B * 384)) || (rc = A(&ws->q_c, B * 384)) ||
+      (rc = A(&ws->hidden_c, B * 384)) || (rc = A(&ws->tmp_c, B * 384)) ||
       (rc = A(&ws->ctx_c, B * 384)) || (rc = A(&ws->g_c, B * 1536)) || (rc = A(&ws->out_c, B * 384)) ||
       (rc = A(&ws->act_q_c, B * 384)) || (rc = A(&ws->act_scale_c, B)) || (rc = A(&ws->rowmax_ctx_c, B)) ||
       (rc = A(&ws->rowmax_g_c, B)))

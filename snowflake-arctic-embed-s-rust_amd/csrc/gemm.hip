@@ -256,21 +256,21 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
 
 // ---------------------------------------------------------------------------
 // Small M (latency-bound launches: single sequences, short batches, the
-// layer-11 tail): 16 rows per workgroup of 8 waves.  The workgroup stages its
-// whole A tile (16 x K int8; f32 A is quantized on the way, as astore does
-// above; kALn: through a LayerNorm) into LDS once, so the K loop has no
-// barrier; each wave streams its B fragments through a register ring kRing K
-// steps deep.
+// layer-11 tail): 16 rows per workgroup of 8 waves.  The workgroup
+// stages its whole A tile (16 x K int8; f32 A is quantized on the way, as astore
+// does above; kALn: through a LayerNorm; kAPreLn: a LayerNorm of the rows of a
+// first GEMM) into LDS once, so the K loop has no barrier; each wave streams its
+// B fragments through a register ring kRing K steps deep.
 //
-// The 8 waves form CG = 8 / KS column groups of 48 columns, and the KS waves of
-// a group split K: wave w takes column group w % CG and K steps
+// The 8 waves form CG = 8 / KS column groups of 48 columns, and the KS waves
+// of a group split K: wave w takes column group w % CG and K steps
 // [(w / CG) KT / KS, (w / CG + 1) KT / KS).  Their int32 partial sums (exact in
 // any order) meet in LDS, and each of them applies the epilogue to 16 / KS of
 // the 16 rows.  KS = 1: the workgroup spans 384 columns (with LN it applies the
 // LayerNorm + SmoothQuant of `ln` to its 16 output rows, reference
 // src/simd_math.rs:208-247, and p.out is not written); KS = 2: 192 columns;
-// KS = 8: 48 columns, for long K (a workgroup streams an eighth of the weights
-// of the KS = 1 form).
+// KS = 8: long K, 48 columns (a workgroup streams an eighth of the weights of
+// the KS = 1 form).
 // ---------------------------------------------------------------------------
 constexpr int kSmallMaxK = 1536;
 constexpr int kSmallPitch = kSmallMaxK + 16;  // LDS bytes per A row: conflict-free fragment reads
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   // for the weights.  The A tile is 16 rows x K as 16-byte chunks (16 k-values);
   // thread t takes chunks t + 512 i (kALn: f32 columns 4 (sub + 32 i) .. +3 of
   // row tid / 32).
-  constexpr int kChunks = 16 * kSmallMaxK / 16 / kThreads;  // per thread at the largest K
+  constexpr int kChunks = (16 * kSmallMaxK / 16 + kThreads - 1) / kThreads;  // per thread at the largest K
   const int cpr = p.K >> 4, nch = 16 * cpr;                // chunks per row, in the tile
   const int rr = tid >> 5, sub = tid & 31, lrow = m0 + rr;  // kALn: row and column group
   float4 xv[3], lg[3], lb[3], lsm[3];                       // kALn: x, gamma, beta, inv_smooth

@@ -80,6 +80,10 @@ struct LnArgs {
   float* scale;     // [T]
   uint32_t* rowmax_init;   // optional: set to bits(1e-8f) for each row
   uint32_t* rowmax_init2;  // optional second buffer
+  // kLnSrcEmb, optional: set to bits(1e-8f) for rows < n_c (the layer-11 [CLS] rows' buffers)
+  uint32_t* rowmax_c;
+  uint32_t* rowmax_c2;
+  int n_c;
   // kLnSrcEmb, optional: bit 0 of *err is set when cu is not a prefix sum of T
   // with every segment 1..max_len tokens long (rows are still clamped in bounds)
   int max_len;
@@ -182,21 +186,22 @@ struct ClsArgs {
   int B;
   const int* cu;
   const float* hidden;     // [T,384]
-  const int8_t* act_q;     // [T,384]
+  const int8_t* act_q;     // [T,384] (the layer input, quantized)
   const float* act_scale;  // [T]
-  float* hidden_c;         // [B,384]
-  int8_t* act_q_c;         // [B,384]
-  float* act_scale_c;      // [B]
-  uint32_t* rowmax_init;   // [B] ctx row-absmax buffer to reset
-  uint32_t* rowmax_init2;  // [B] GELU row-absmax buffer to reset, or null
-  const float* q_c;        // [B,384]
+  float* hidden_c;         // [B,384]: the [CLS] rows of hidden, gathered
+  const int8_t* wq;        // q_only linear: swizzled [384,384] int8, w_scale, bias
+  const float* wq_scale;
+  const float* wq_bias;
   const float* kv;         // [T,768]
   float* ctx_c;            // [B,384]
   const float* smooth;     // attn_out inv_smooth
-  uint32_t* rowmax_ctx_c;  // [B]
+  uint32_t* rowmax_ctx_c;  // [B], pre-set to bits(1e-8f)
   int max_len = 512;       // keys attended per sequence (<= 512): sizes the V tile in LDS
 };
-void launch_cls(const ClsArgs& p, int stage, hipStream_t st);
+// the layer-11 [CLS] attention: per (sequence, head) the [CLS] row's q (the q_only
+// GEMM for that row and head), its attention over the segment's K/V rows, ctx_c
+// and its row absmax; the head-0 workgroups also gather hidden_c
+void launch_cls(const ClsArgs& p, hipStream_t st);
 void launch_final_ln_l2(int B, const float* src, const float* gamma, const float* beta, float* out, hipStream_t st);
 void launch_fill_u32(uint32_t* dst, int n, uint32_t v, hipStream_t st);
 void launch_gelu_map(const float* x, float* y, size_t n, hipStream_t st);

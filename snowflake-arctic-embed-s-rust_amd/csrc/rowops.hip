@@ -150,6 +150,10 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
       p.scale[row] = max_abs / 127.0f;
       if (p.rowmax_init) p.rowmax_init[row] = __float_as_uint(1e-8f);
       if (p.rowmax_init2) p.rowmax_init2[row] = __float_as_uint(1e-8f);
+      if (SRC == kLnSrcEmb && row < p.n_c) {
+        if (p.rowmax_c) p.rowmax_c[row] = __float_as_uint(1e-8f);
+        if (p.rowmax_c2) p.rowmax_c2[row] = __float_as_uint(1e-8f);
+      }
     }
   }
 }
