@@ -277,7 +277,7 @@ constexpr int kSmallPitch = kSmallMaxK + 16;  // LDS bytes per A row: conflict-f
 constexpr int kLnPitchS = 388;                // LDS floats per row of the fused LayerNorm
 constexpr int kEPitchS = 52;                  // LDS words per row of a wave's epilogue staging tile
 
-template <int AM, int EM, bool LN, int KS>
+template <int AM, int EM, bool LN, int KS, int RT = 16>
 __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, PreArgs pre) {
   constexpr int WAVES = 8, NW = 48, kThreads = 512;
   constexpr int CG = WAVES / KS, kBN = CG * NW, kCB = NW / 16, kF4 = NW / 4;
@@ -285,6 +285,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   constexpr int kRing = KS == 1 ? 6 : 3;  // B ring depth (K steps in flight per wave)
   constexpr bool kLnIn = AM == kALn || AM == kAPreLn;  // a LayerNorm in front of the GEMM
   static_assert(KS == 1 || KS == 2 || KS == 8, "K splits");
+  static_assert(RT == 16 || (RT == 8 && KS == 8 && !LN && AM != kALn && AM != kAPreLn), "8-row tiles: KS = 8 only");
   static_assert(!LN || (KS == 1 && EM == kEpiF32), "fused LayerNorm: 16 rows x 384 columns");
   static_assert(!kLnIn || !LN, "LayerNorm prologue or epilogue");
   constexpr bool kLnTile = LN || kLnIn;  // an f32 row tile for a LayerNorm
@@ -298,8 +299,9 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   __shared__ float s_pre_sa[16];  // kAPreLn: the first GEMM's row scales
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fk = (lane >> 4) * 16;
-  const int mt = (p.M + 15) >> 4;
-  const int m0 = (blockIdx.x % mt) * 16, n0 = (blockIdx.x / mt) * kBN;
+  // RT rows per tile (RT = 8: the MFMA's rows 8-15 read zeros and are not stored)
+  const int mt = (p.M + RT - 1) / RT;
+  const int m0 = (blockIdx.x % mt) * RT, n0 = (blockIdx.x / mt) * kBN;
   const int NB = p.N >> 4;
   const int cg = wave % CG, ks = wave / CG;
   const int col0 = n0 + cg * NW;
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   // thread t takes chunks t + 512 i (kALn: f32 columns 4 (sub + 32 i) .. +3 of
   // row tid / 32).
   constexpr int kChunks = (16 * kSmallMaxK / 16 + kThreads - 1) / kThreads;  // per thread at the largest K
-  const int cpr = p.K >> 4, nch = 16 * cpr;                // chunks per row, in the tile
+  const int cpr = p.K >> 4, nch = RT * cpr;                // chunks per row, in the tile
   const int rr = tid >> 5, sub = tid & 31, lrow = m0 + rr;  // kALn: row and column group
   float4 xv[3], lg[3], lb[3], lsm[3];                       // kALn: x, gamma, beta, inv_smooth
   v4i qa[kChunks];                                          // kAI8
@@ -427,6 +429,12 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
 
   // the A tile into LDS: int8 A as loaded, f32 A quantized as astore does above,
   // kALn through the LayerNorm; kAPreLn: the first GEMM's rows, then the LayerNorm
+  if constexpr (RT < 16) {  // the tile's unused rows: zeros
+    for (int c = tid; c < (16 - RT) * cpr; c += kThreads) {
+      const int r = RT + c / cpr;
+      *reinterpret_cast<v4i*>(&sA[r * kSmallPitch + (c % cpr) * 16]) = v4i{0, 0, 0, 0};
+    }
+  }
   if constexpr (AM == kAPreLn) {
     // its A tile (quantized as kAF32QSmooth) and row scales
     if (tid < 384) {
@@ -614,7 +622,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   for (int k = 0; k < kEk; k++) {
     int er, c4;
     epos(k, er, c4);
-    const bool valid = lane + 64 * k < kPos;  // wave-uniform in k; per lane at the last k
+    const bool valid = lane + 64 * k < kPos && er < RT;  // uniform in k but the last; rows < RT
     const int row = m0 + er, col = col0 + c4 * 4;
     int4 a4 = *reinterpret_cast<const int4*>(&sE[cg][er * kEPitchS + c4 * 4]);
 #pragma unroll
@@ -646,7 +654,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
     else if (valid && row < p.M) *reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col) = v;
   }
   wave_lds_sync();
-  if (EM == kEpiGelu && lane < RPW && m0 + ks * RPW + lane < p.M)
+  if (EM == kEpiGelu && lane < RPW && ks * RPW + lane < RT && m0 + ks * RPW + lane < p.M)
     atomicMax(&p.g_rowmax[m0 + ks * RPW + lane], sRowMax[wave][lane]);
   if constexpr (LN) {
     // sequential sums per row (one lane each), then 32 lanes per row normalize
@@ -744,8 +752,12 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
     if (ln) {
       hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, true, 1>), dim3(mt16), dim3(512), 0, st, p, *ln, PreArgs{});
     } else if (EM == kEpiF32 && p.K >= kSplitMinK && p.K % 512 == 0) {
-      hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, false, 8>), dim3(mt16 * (p.N / 48)), dim3(512), 0, st, p,
-                         LnArgs{}, PreArgs{});
+      if (AM != kAI8 && mt16 * (p.N / 48) < 256)  // 8-row tiles: half the f32 A per workgroup, twice the workgroups
+        hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, false, 8, 8>), dim3(((p.M + 7) / 8) * (p.N / 48)),
+                           dim3(512), 0, st, p, LnArgs{}, PreArgs{});
+      else
+        hipLaunchKernelGGL((gemm_small_kernel<AM, kEpiF32, false, 8>), dim3(mt16 * (p.N / 48)), dim3(512), 0, st, p,
+                           LnArgs{}, PreArgs{});
     } else {
       hipLaunchKernelGGL((gemm_small_kernel<AM, EM, false, 2>), dim3(mt16 * (p.N / 192)), dim3(512), 0, st, p,
                          LnArgs{}, PreArgs{});
