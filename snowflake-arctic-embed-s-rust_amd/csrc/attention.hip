@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
 
 // ---------------------------------------------------------------------------
 // Latency form, for batches of few tiles (a single sequence, the latency entry
-// points): one workgroup of 8 waves per (sequence, 16 queries, head), with the
+// points): one workgroup of 8 waves per (sequence, 8 queries, head), with the
 // arithmetic of attention_kernel<true> in the same order, laid out for a short
 // critical path rather than for throughput:
 //  * every global load (the Q operands, the K operands of the wave's key
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
 //    key order from LDS.
 // dynamic LDS: S[16][s_pitch] scores -> exps, then V[s_pitch - 4][32]
 // ---------------------------------------------------------------------------
-constexpr int kLatQ = 16;  // queries per workgroup
+constexpr int kLatQ = 8;  // queries per workgroup (MFMA rows 8-15 repeat a query and are not used)
 
 __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tiles_per_seq) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -529,8 +529,8 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
       f[4 * c] = v.x; f[4 * c + 1] = v.y; f[4 * c + 2] = v.z; f[4 * c + 3] = v.w;
     }
   };
-  float qf[8];  // query q0 + lr (rows past the segment clamped)
-  load_dims(qkv + (size_t)min(q0 + lr, L - 1) * HQKV, qf);
+  float qf[8];  // query q0 + lr (rows past the segment, and lr >= kLatQ, clamped)
+  load_dims(qkv + (size_t)min(q0 + min(lr, kLatQ - 1), L - 1) * HQKV, qf);
   const int nkb = (L + 15) >> 4;  // <= 32: at most 4 blocks per wave
   float kf[4][8];
 #pragma unroll
@@ -574,13 +574,15 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
       sc.y = acc[1] * kInvSqrtD;
       sc.z = acc[2] * kInvSqrtD;
       sc.w = acc[3] * kInvSqrtD;
-      *reinterpret_cast<float4*>(&S[lr * pitch + 16 * kb + 4 * lg]) = sc;  // < round16(L) <= lmax
-      m = fmaxf(fmaxf(m, fmaxf(sc.x, sc.y)), fmaxf(sc.z, sc.w));
+      if (lr < kLatQ) {
+        *reinterpret_cast<float4*>(&S[lr * pitch + 16 * kb + 4 * lg]) = sc;  // < round16(L) <= lmax
+        m = fmaxf(fmaxf(m, fmaxf(sc.x, sc.y)), fmaxf(sc.z, sc.w));
+      }
     }
   }
   m = fmaxf(m, __shfl_xor(m, 16, 64));
   m = fmaxf(m, __shfl_xor(m, 32, 64));
-  if (lane < 16) s_maxw[wave][lane] = m;
+  if (lane < kLatQ) s_maxw[wave][lane] = m;
 #pragma unroll
   for (int i = 0; i < kVF; i++) {
     const int f = tid + 512 * i;
