@@ -723,8 +723,7 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
     // is a non-NaN >= +0 where fmaxf is the reference's scan), by atomicMax on
     // the f32 bits
     float a = q < nq ? nanless_max(0.0f, fabsf(o * p.smooth[h * 32 + d])) : 0.0f;
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+    a = lanes32_max(a);
     if (d == 0 && q < nq) atomicMax(&p.rowmax[s0 + q0 + q], __float_as_uint(a));
   }
 }

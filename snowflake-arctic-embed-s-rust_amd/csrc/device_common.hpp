@@ -77,6 +77,20 @@ __device__ __forceinline__ float row16_max(float m) {
   return fmaxf(m, __uint_as_float(dpp<kDppMirror>(__float_as_uint(m))));
 }
 
+// max over this lane's group of 8 lanes (DPP; every lane gets it)
+__device__ __forceinline__ float lanes8_max(float m) {
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor1>(__float_as_uint(m))));
+  m = fmaxf(m, __uint_as_float(dpp<kDppXor2>(__float_as_uint(m))));
+  return fmaxf(m, __uint_as_float(dpp<kDppHalfMirror>(__float_as_uint(m))));
+}
+
+// max over this lane's half-wave of 32 lanes (every lane gets it): DPP within
+// each 16-lane row, then one cross-row exchange
+__device__ __forceinline__ float lanes32_max(float m) {
+  m = row16_max(m);
+  return fmaxf(m, __shfl_xor(m, 16, 64));
+}
+
 // Orders this wave's LDS accesses before and after it (LDS data private to one
 // wave needs no workgroup barrier: a wave's LDS operations complete in order once
 // the counter is drained).

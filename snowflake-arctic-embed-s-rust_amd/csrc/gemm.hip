@@ -306,7 +306,8 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
   const int cg = wave % CG, ks = wave / CG;
   const int col0 = n0 + cg * NW;
   // this wave's K steps [kb0, kb0 + KT)
-  const int KT = (p.K >> 6) / KS, kb0 = ks * KT;
+  // (KS need not divide the K steps: wave ks takes [ks KTT / KS, (ks + 1) KTT / KS))
+  const int KTT = p.K >> 6, kb0 = ks * KTT / KS, KT = (ks + 1) * KTT / KS - kb0;
   const ExpTab tb = exp_tab_regs();  // the epilogue below is wave-uniform
 
   // The A tile's global loads go out first, then the B ring and the epilogue
@@ -534,8 +535,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
       amax = nanless_max(amax, fabsf(ys[i].z));
       amax = nanless_max(amax, fabsf(ys[i].w));
     }
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+    amax = lanes32_max(amax);  // amax is never NaN: fmaxf is nanless_max here
     const float max_abs = nanless_max(1e-8f, amax);
     const float inv_scale = 127.0f / max_abs;
 #pragma unroll
@@ -709,8 +709,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
       amax = nanless_max(amax, fabsf(ys[i].z));
       amax = nanless_max(amax, fabsf(ys[i].w));
     }
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+    amax = lanes32_max(amax);  // amax is never NaN: fmaxf is nanless_max here
     const float max_abs = nanless_max(1e-8f, amax);
     const float inv_scale = 127.0f / max_abs;
     if (row < p.M) {

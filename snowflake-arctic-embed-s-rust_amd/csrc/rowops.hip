@@ -134,8 +134,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
     amax = nanless_max(amax, fabsf(ys[i].z));
     amax = nanless_max(amax, fabsf(ys[i].w));
   }
-#pragma unroll
-  for (int off = 1; off < 8; off <<= 1) amax = nanless_max(amax, __shfl_xor(amax, off, 64));
+  amax = lanes8_max(amax);  // amax is never NaN: fmaxf is nanless_max here
   const float max_abs = nanless_max(1e-8f, amax);
   const float inv_scale = 127.0f / max_abs;
   if (valid) {
