@@ -430,7 +430,11 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
                                         ws->rowmax_ctx, T, ws->rowmax_g),
                                 kEpiF32, st);
       } else {
-        gemm(D.qkv, T, ws->act_q, kAI8, ws->act_scale, nullptr, nullptr, nullptr, ws->qkv, kEpiF32, nullptr, nullptr);
+        GemmArgs g = gemm_args(D.qkv, T, ws->act_q, ws->act_scale, nullptr, nullptr, nullptr, ws->qkv, nullptr, nullptr);
+        // Q is read once by the attention; K and V many times: only K and V
+        // are left in the Infinity Cache
+        g.stream_cols = 384;
+        launch_gemm(g, kAI8, kEpiF32, st);
       }
     }
     {

@@ -255,6 +255,131 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
 }
 
 // ---------------------------------------------------------------------------
+// int8 A, K = 384, f32 epilogue without residual, many rows (the QKV GEMM):
+// A-stationary.  A workgroup of 4 waves stages its 64-row A tile (64 x 384 int8)
+// in LDS once and walks every 192-column tile of N with it, so A leaves HBM once
+// instead of once per column tile.  Each column tile's W fragments (6 K steps x
+// 3 per wave) stream from L2 into registers; the next tile's are issued into the
+// same registers once this tile's MFMAs are done, before its epilogue.  The
+// arithmetic is gemm_w8a8_kernel's.
+// ---------------------------------------------------------------------------
+constexpr int kAsPitch = 384 + 16;  // LDS bytes per A row: conflict-free fragment reads
+
+__global__ __launch_bounds__(256, 2) void gemm_astat_kernel(GemmArgs p) {
+  constexpr int kCB = 3, kF4 = 12, kEk = 3;  // 48 columns per wave
+  __shared__ __attribute__((aligned(16))) int8_t sA[kBM * kAsPitch];
+  __shared__ __attribute__((aligned(16))) int sE[4][16 * kEPitch];
+  __shared__ float sEpSa[kBM];
+  __shared__ __attribute__((aligned(16))) float sWs[2][192], sB[2][192];  // w_scale / bias of column tiles c, c + 1
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fk = (lane >> 4) * 16;
+  // row tiles last to first: the rows written last (still in the Infinity Cache
+  // when the next kernel starts) are the batch's first, which attention reads first
+  const int m0 = (gridDim.x - 1 - blockIdx.x) * kBM, nt = p.N / 192, NB = p.N >> 4;
+  const int8_t* A = reinterpret_cast<const int8_t*>(p.A);
+  // the A tile: chunk c = tid + 256 i of 16 bytes is row c / 24, k 16 (c % 24)
+  v4i ach[6];
+#pragma unroll
+  for (int i = 0; i < 6; i++) {
+    const int c = tid + 256 * i;
+    ach[i] = *reinterpret_cast<const v4i*>(A + (size_t)min(m0 + c / 24, p.M - 1) * 384 + (c % 24) * 16);
+  }
+  const float sa_t = tid < kBM ? p.a_scale[min(m0 + tid, p.M - 1)] : 0.0f;
+  // W fragments of column tile c for this wave; the tile's w_scale / bias go to
+  // LDS (threads 0-47: w_scale float4s, 48-95: bias float4s)
+  const int8_t* wbase = p.w + (size_t)lane * 16;
+  v4i bf[6][kCB];
+  auto wload = [&](int c) {
+    const int cb0 = (c * 192 + wave * 48) >> 4;
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++)
+#pragma unroll
+      for (int j = 0; j < kCB; j++)
+        bf[kt][j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + cb0 + j) * 1024);
+  };
+  auto eload = [&](int c) {  // returns this thread's float4 (threads < 96)
+    if (tid < 48) return reinterpret_cast<const float4*>(p.w_scale + c * 192)[tid];
+    if (tid < 96) return reinterpret_cast<const float4*>(p.bias + c * 192)[tid - 48];
+    return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  };
+  auto estore = [&](int buf, const float4& v) {
+    if (tid < 48) reinterpret_cast<float4*>(sWs[buf])[tid] = v;
+    else if (tid < 96) reinterpret_cast<float4*>(sB[buf])[tid - 48] = v;
+  };
+  wload(0);
+  estore(0, eload(0));
+#pragma unroll
+  for (int i = 0; i < 6; i++) {
+    const int c = tid + 256 * i;
+    *reinterpret_cast<v4i*>(&sA[(c / 24) * kAsPitch + (c % 24) * 16]) = ach[i];
+  }
+  if (tid < kBM) sEpSa[tid] = sa_t;
+  __syncthreads();
+
+  int* E = sE[wave];
+  for (int c = 0; c < nt; c++) {  // workgroup-uniform
+    v4i acc[4][kCB];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < kCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++) {
+      v4i af[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAsPitch + kt * 64 + fk]);
+#pragma unroll
+      for (int j = 0; j < kCB; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt][j], acc[i][j], 0, 0, 0);
+    }
+    float4 en = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (c + 1 < nt) {  // the next tile's operands, into the registers just released
+      wload(c + 1);
+      en = eload(c + 1);
+    }
+    const float* ws = sWs[c & 1];
+    const float* bs = sB[c & 1];
+    // epilogue, one 16-row block at a time through this wave's LDS tile
+    const int col0 = c * 192 + wave * 48;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int j = 0; j < kCB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) E[((lane >> 4) * 4 + r) * kEPitch + j * 16 + fr] = acc[i][j][r];
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < kEk; k++) {
+        const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx % kF4;
+        const int row = m0 + i * 16 + rr;
+        const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
+        const float sa = sEpSa[i * 16 + rr];
+        const float4 w4 = *reinterpret_cast<const float4*>(&ws[wave * 48 + c4 * 4]);
+        const float4 b4 = *reinterpret_cast<const float4*>(&bs[wave * 48 + c4 * 4]);
+        float4 v;
+        v.x = fmaf((float)a4.x, sa * w4.x, b4.x);
+        v.y = fmaf((float)a4.y, sa * w4.y, b4.y);
+        v.z = fmaf((float)a4.z, sa * w4.z, b4.z);
+        v.w = fmaf((float)a4.w, sa * w4.w, b4.w);
+        if (row < p.M) {
+          float4* dst = reinterpret_cast<float4*>(p.out + (size_t)row * p.N + col0 + c4 * 4);
+          if (col0 < p.stream_cols)  // wave-uniform
+            __builtin_nontemporal_store(v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z),
+                                            __float_as_int(v.w)},
+                                        reinterpret_cast<v4i*>(dst));
+          else
+            *dst = v;
+        }
+      }
+      wave_lds_sync();
+    }
+    if (c + 1 < nt) estore((c + 1) & 1, en);
+    __syncthreads();  // tile c + 1's w_scale / bias are in LDS; tile c's are no longer read
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small M (latency-bound launches: single sequences, short batches, the
 // layer-11 tail): 16 rows per workgroup of 8 waves.  The workgroup
 // stages its whole A tile (16 x K int8; f32 A is quantized on the way, as astore
@@ -761,6 +886,10 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
       hipLaunchKernelGGL((gemm_small_kernel<AM, EM, false, 2>), dim3(mt16 * (p.N / 192)), dim3(512), 0, st, p,
                          LnArgs{}, PreArgs{});
     }
+    return;
+  }
+  if (AM == kAI8 && EM == kEpiF32 && p.K == 384 && !p.res && p.N % 192 == 0) {
+    hipLaunchKernelGGL(gemm_astat_kernel, dim3((p.M + kBM - 1) / kBM), dim3(256), 0, st, p);
     return;
   }
   p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;

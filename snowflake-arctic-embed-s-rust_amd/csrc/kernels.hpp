@@ -32,6 +32,7 @@ struct GemmArgs {
   const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
   uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
   int col_fast;               // set by launch_gemm: workgroup order (column tile fastest)
+  int stream_cols = 0;        // output columns [0, stream_cols) are stored nontemporally (read once later)
 };
 // N % 384 == 0, K % 64 == 0
 void launch_gemm(const GemmArgs& p, int amode, int emode, hipStream_t st);
