@@ -898,8 +898,6 @@ void init_attention_kernels() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(cls_attention_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)(sizeof(float) * 32 * 512));
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lat_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)(sizeof(float) * (16 * (size_t)attention_pitch(512) + 32 * 512)));
@@ -997,16 +995,17 @@ void launch_attention_short(const AttnArgs& p, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // one workgroup (4 waves) per (sequence, head): the [CLS] query attends to its
 // segment with the same exact scalar order as attention_kernel
-// (src/model.rs:814-843).  Every global load is issued at the start: the [CLS]
-// row's int8 activations and the head's q_only weight fragments, the K rows of
-// the thread's keys (tid, tid + 256) and the segment's V rows, which go to LDS
-// ([key][32], dynamic, p.max_len keys) for the in-order PV sums.  Wave 0 forms
-// the head's 32 q values as the q_only GEMM does for that row (int8 MFMA with
-// the [CLS] row as row 0 of the A tile, then fma(f32(acc), sa * ws, bias)).
-// Keys past p.max_len (<= 512) are not attended (the embedding kernel reports
-// such sequences through the workspace's error word).
+// (src/model.rs:814-843).  The global loads of the [CLS] row's int8
+// activations, the head's q_only weight fragments and the K rows of the
+// thread's keys (tid, tid + 256) are issued at the start.  Wave 0 forms the
+// head's 32 q values as the q_only GEMM does for that row (int8 MFMA with the
+// [CLS] row as row 0 of the A tile, then fma(f32(acc), sa * ws, bias)).  The PV
+// lanes read V from global memory through a register ring 16 keys ahead, its
+// first loads issued before the softmax phases, so the workgroup needs no large
+// LDS tile and many fit on a CU.  Keys past p.max_len (<= 512) are not attended
+// (the embedding kernel reports such sequences through the workspace's error
+// word).
 __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
-  extern __shared__ __attribute__((aligned(16))) float sV[];  // [L][32]
   __shared__ __attribute__((aligned(16))) float S[512];
   __shared__ __attribute__((aligned(16))) float sQ[32];
   __shared__ float s_m[4];
@@ -1030,14 +1029,6 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   }
   if (h == 0 && tid < 96)  // gather the [CLS] row of hidden (the tail's residual)
     reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[tid] = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[tid];
-  // V: float4 f = tid + 256 i is key f / 8, dims 4 (f % 8) .. +3
-  constexpr int kVF = 512 * 8 / 256;
-  float4 vr[kVF];
-#pragma unroll
-  for (int i = 0; i < kVF; i++) {
-    const int f = tid + 256 * i;
-    if (f < 8 * L) vr[i] = *reinterpret_cast<const float4*>(p.kv + (size_t)(s0 + f / 8) * 2 * H + H + h * 32 + (f % 8) * 4);
-  }
   float4 kr[2][8];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -1061,11 +1052,6 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
         sQ[16 * j + lane] = fmaf((float)acc[j][0], sa * p.wq_scale[col], p.wq_bias[col]);
       }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < kVF; i++) {
-    const int f = tid + 256 * i;
-    if (f < 8 * L) *reinterpret_cast<float4*>(&sV[4 * f]) = vr[i];
   }
   __syncthreads();
   float q[32];
@@ -1096,6 +1082,20 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
   if (lane == 0) s_m[wave] = m;
+  // the PV lanes' first V values (keys 0-15, dim `lane`; rows past the segment
+  // clamped), issued now so that their latency hides behind the softmax
+  const float* vcol = p.kv + (size_t)s0 * 2 * H + H + h * 32 + (lane & 31);
+  const int nvb = L >> 3;  // full batches of 8 keys
+  float va[8], vb[8];
+  auto ldv = [&](int bi, float (&v)[8]) {
+    const int t0 = 8 * min(bi, max(nvb - 1, 0));
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = vcol[(size_t)min(t0 + k, L - 1) * 2 * H];
+  };
+  if (wave == 0 && L > 0) {
+    ldv(0, va);
+    ldv(1, vb);
+  }
   __syncthreads();
   m = nanless_max(nanless_max(s_m[0], s_m[1]), nanless_max(s_m[2], s_m[3]));
 #pragma unroll
@@ -1105,14 +1105,37 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
     if (j < L) S[j] = e;
   }
   __syncthreads();
-  if (tid == 0) {  // in-order denominator
+  if (tid == 0) {  // in-order denominator; batches of 16 keys, each read while the previous one is added
     float sum = 0.0f;
-    int j = 0;
-    for (; j + 4 <= L; j += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(&S[j]);
-      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+    const int nb = L >> 4;
+    float4 ea[4], eb[4];
+    auto ld = [&](int bi, float4 (&v)[4]) {
+      const float4* src = reinterpret_cast<const float4*>(&S[16 * min(bi, nb - 1)]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = src[i];
+    };
+    auto add = [&](const float4 (&v)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sum += v[i].x; sum += v[i].y; sum += v[i].z; sum += v[i].w;
+      }
+    };
+    if (nb > 0) {
+      ld(0, ea);
+      int bi = 0;
+      for (; bi + 2 <= nb; bi += 2) {
+        ld(bi + 1, eb);
+        __builtin_amdgcn_sched_barrier(0);
+        add(ea);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(bi + 2, ea);
+        __builtin_amdgcn_sched_barrier(0);
+        add(eb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (bi < nb) add(ea);
     }
-    for (; j < L; j++) sum += S[j];
+    for (int j = 16 * nb; j < L; j++) sum += S[j];
     s_inv = 1.0f / sum;
   }
   __syncthreads();
@@ -1125,16 +1148,28 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   __syncthreads();
   if (wave == 0) {
     float o = 0.0f;
-    if (lane < 32) {  // ctx_d = sum_t p_t * v_t,d in order
-      int t = 0;
-      for (; t + 4 <= L; t += 4) {
-        const float4 pt = *reinterpret_cast<const float4*>(&S[t]);
-        o = o + pt.x * sV[32 * t + lane];
-        o = o + pt.y * sV[32 * (t + 1) + lane];
-        o = o + pt.z * sV[32 * (t + 2) + lane];
-        o = o + pt.w * sV[32 * (t + 3) + lane];
+    if (lane < 32) {  // ctx_d = sum_t p_t * v_t,d in order; V two batches of 8 keys ahead
+      auto add = [&](int bi, const float (&v)[8]) {
+        const float4 p0 = *reinterpret_cast<const float4*>(&S[8 * bi]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&S[8 * bi + 4]);
+        o = o + p0.x * v[0];
+        o = o + p0.y * v[1];
+        o = o + p0.z * v[2];
+        o = o + p0.w * v[3];
+        o = o + p1.x * v[4];
+        o = o + p1.y * v[5];
+        o = o + p1.z * v[6];
+        o = o + p1.w * v[7];
+      };
+      int bi = 0;
+      for (; bi + 2 <= nvb; bi += 2) {  // va holds batch bi, vb batch bi + 1
+        add(bi, va);
+        ldv(bi + 2, va);
+        add(bi + 1, vb);
+        ldv(bi + 3, vb);
       }
-      for (; t < L; t++) o = o + S[t] * sV[32 * t + lane];
+      if (bi < nvb) add(bi, va);
+      for (int t = 8 * nvb; t < L; t++) o = o + S[t] * vcol[(size_t)t * 2 * H];
       p.ctx_c[(size_t)b * H + h * 32 + lane] = o;
     }
     float a = lane < 32 ? fabsf(o * p.smooth[h * 32 + lane]) : 0.0f;
@@ -1145,7 +1180,7 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
 }
 
 void launch_cls(const ClsArgs& p, hipStream_t st) {
-  hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), sizeof(float) * 32 * (size_t)p.max_len, st, p);
+  hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), 0, st, p);
 }
 
 }  // namespace aek
