@@ -26,6 +26,8 @@
 // integer sum is exact.  Output: lane l, register r holds D[4*(l/16)+r][l%16].
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <algorithm>
 
 #include "device_common.hpp"
@@ -256,35 +258,37 @@ __global__ __launch_bounds__(256, NW == 96 ? 2 : (AM == kAI8 ? 4 : 3)) void gemm
 
 // ---------------------------------------------------------------------------
 // int8 A, K = 384, f32 epilogue without residual, many rows (the QKV GEMM):
-// A-stationary.  A workgroup of 4 waves stages its 64-row A tile (64 x 384 int8)
-// in LDS once and walks every 192-column tile of N with it, so A leaves HBM once
-// instead of once per column tile.  Each column tile's W fragments (6 K steps x
+// A-stationary.  A workgroup of 4 waves stages its A tile (16 RB rows x 384
+// int8) in LDS once and walks every 192-column tile of N with it, so A leaves
+// HBM once instead of once per column tile.  Each column tile's W fragments (6 K steps x
 // 3 per wave) stream from L2 into registers; the next tile's are issued into the
 // same registers once this tile's MFMAs are done, before its epilogue.  The
 // arithmetic is gemm_w8a8_kernel's.
 // ---------------------------------------------------------------------------
 constexpr int kAsPitch = 384 + 16;  // LDS bytes per A row: conflict-free fragment reads
 
+template <int RB>
 __global__ __launch_bounds__(256, 2) void gemm_astat_kernel(GemmArgs p) {
   constexpr int kCB = 3, kF4 = 12, kEk = 3;  // 48 columns per wave
-  __shared__ __attribute__((aligned(16))) int8_t sA[kBM * kAsPitch];
+  constexpr int kRows = 16 * RB, kChunks = kRows * 24, kLd = (kChunks + 255) / 256;  // A tile: 16-byte chunks
+  __shared__ __attribute__((aligned(16))) int8_t sA[kRows * kAsPitch];
   __shared__ __attribute__((aligned(16))) int sE[4][16 * kEPitch];
-  __shared__ float sEpSa[kBM];
+  __shared__ float sEpSa[kRows];
   __shared__ __attribute__((aligned(16))) float sWs[2][192], sB[2][192];  // w_scale / bias of column tiles c, c + 1
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fk = (lane >> 4) * 16;
   // row tiles last to first: the rows written last (still in the Infinity Cache
   // when the next kernel starts) are the batch's first, which attention reads first
-  const int m0 = (gridDim.x - 1 - blockIdx.x) * kBM, nt = p.N / 192, NB = p.N >> 4;
+  const int m0 = (gridDim.x - 1 - blockIdx.x) * kRows, nt = p.N / 192, NB = p.N >> 4;
   const int8_t* A = reinterpret_cast<const int8_t*>(p.A);
   // the A tile: chunk c = tid + 256 i of 16 bytes is row c / 24, k 16 (c % 24)
-  v4i ach[6];
+  v4i ach[kLd];
 #pragma unroll
-  for (int i = 0; i < 6; i++) {
-    const int c = tid + 256 * i;
+  for (int i = 0; i < kLd; i++) {
+    const int c = min(tid + 256 * i, kChunks - 1);
     ach[i] = *reinterpret_cast<const v4i*>(A + (size_t)min(m0 + c / 24, p.M - 1) * 384 + (c % 24) * 16);
   }
-  const float sa_t = tid < kBM ? p.a_scale[min(m0 + tid, p.M - 1)] : 0.0f;
+  const float sa_t = tid < kRows ? p.a_scale[min(m0 + tid, p.M - 1)] : 0.0f;
   // W fragments of column tile c for this wave; the tile's w_scale / bias go to
   // LDS (threads 0-47: w_scale float4s, 48-95: bias float4s)
   const int8_t* wbase = p.w + (size_t)lane * 16;
@@ -309,29 +313,29 @@ __global__ __launch_bounds__(256, 2) void gemm_astat_kernel(GemmArgs p) {
   wload(0);
   estore(0, eload(0));
 #pragma unroll
-  for (int i = 0; i < 6; i++) {
+  for (int i = 0; i < kLd; i++) {
     const int c = tid + 256 * i;
-    *reinterpret_cast<v4i*>(&sA[(c / 24) * kAsPitch + (c % 24) * 16]) = ach[i];
+    if (kChunks % 256 == 0 || c < kChunks) *reinterpret_cast<v4i*>(&sA[(c / 24) * kAsPitch + (c % 24) * 16]) = ach[i];
   }
-  if (tid < kBM) sEpSa[tid] = sa_t;
+  if (tid < kRows) sEpSa[tid] = sa_t;
   __syncthreads();
 
   int* E = sE[wave];
   for (int c = 0; c < nt; c++) {  // workgroup-uniform
-    v4i acc[4][kCB];
+    v4i acc[RB][kCB];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < RB; i++)
 #pragma unroll
       for (int j = 0; j < kCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int kt = 0; kt < 6; kt++) {
-      v4i af[4];
+      v4i af[RB];
 #pragma unroll
-      for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAsPitch + kt * 64 + fk]);
+      for (int i = 0; i < RB; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAsPitch + kt * 64 + fk]);
 #pragma unroll
       for (int j = 0; j < kCB; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt][j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < RB; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt][j], acc[i][j], 0, 0, 0);
     }
     float4 en = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (c + 1 < nt) {  // the next tile's operands, into the registers just released
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void gemm_astat_kernel(GemmArgs p) {
     // epilogue, one 16-row block at a time through this wave's LDS tile
     const int col0 = c * 192 + wave * 48;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RB; i++) {
 #pragma unroll
       for (int j = 0; j < kCB; j++)
 #pragma unroll
@@ -856,6 +860,19 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
 
 // Up to this many rows (and K <= kSmallMaxK) the GEMMs take gemm_small_kernel.
 constexpr int kSmallM = 1024;
+
+// compute units of the current device (cached per device; 256 on MI355X)
+static int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 // int8 A of more bytes than this is re-read from HBM if each column tile walks
 // all row tiles (measured: 113 MB of A at M = 294,912 runs 8-12 % faster column
 // tile fastest, 25 MB at M = 65,536 up to 13 % slower)
@@ -889,7 +906,14 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
     return;
   }
   if (AM == kAI8 && EM == kEpiF32 && p.K == 384 && !p.res && p.N % 192 == 0) {
-    hipLaunchKernelGGL(gemm_astat_kernel, dim3((p.M + kBM - 1) / kBM), dim3(256), 0, st, p);
+    // row tiles of 48 or 64 rows, whichever leaves fewer rows' worth of time in
+    // a last, partly filled round of workgroups (2 per CU)
+    const int slots = 2 * device_cu_count();
+    const long t4 = 4L * (((p.M + 63) / 64 + slots - 1) / slots), t3 = 3L * (((p.M + 47) / 48 + slots - 1) / slots);
+    if (t3 < t4)
+      hipLaunchKernelGGL(gemm_astat_kernel<3>, dim3((p.M + 47) / 48), dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL(gemm_astat_kernel<4>, dim3((p.M + 63) / 64), dim3(256), 0, st, p);
     return;
   }
   p.col_fast = AM != kAI8 || (size_t)p.M * p.K > kColFastABytes;
