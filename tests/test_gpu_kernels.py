@@ -86,6 +86,30 @@ def test_gemm_configs1_microbench_shapes(torch_gpu, m, k, n):
     assert np.all(np.isfinite(out))
 
 
+@pytest.mark.parametrize("m,n", [(24576, 1152), (40000, 1152), (32761, 768)])
+def test_gemm_row_stationary_tiles(torch_gpu, m, n):
+    """Many-row int8 GEMMs without residual run A-stationary (an A tile of 48 or 64 rows kept in LDS
+    while the workgroup walks every column tile): 24,576 rows in exactly 512 tiles of 48, 40,000
+    rows (48-row tiles, the last one partial) and 32,761 rows (64-row tiles, the last one partial).
+    Rows of the first, last and random tiles bit for bit against the oracle."""
+    torch = torch_gpu
+    k = 384
+    w, ws, b, s = linear_inputs(n, k, m + n)
+    rng = np.random.default_rng(m)
+    a = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sa = rng.uniform(0.01, 0.1, m).astype(f32)
+    lin = ae.Linear(w, ws, b, s)
+    a_d, sa_d = dev(torch, a), dev(torch, sa)
+    out_d = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    lin.gemm(m, a_d.data_ptr(), sa_d.data_ptr(), None, out_d.data_ptr())
+    torch.cuda.synchronize()
+    out = out_d.cpu().numpy()
+    lin.close()
+    rows = np.unique(np.concatenate([np.arange(72), np.arange(m - 72, m), rng.choice(m, 96, replace=False)]))
+    assert np.array_equal(bits(out[rows]), bits(orc.gemm(a[rows], sa[rows], w, ws, b)))
+    assert np.all(np.isfinite(out))
+
+
 def test_gemm_extreme_accumulators(torch_gpu):
     torch = torch_gpu
     n, k, m = 384, 1536, 3
