@@ -68,10 +68,12 @@ def kernel_work(kind, T, B, lens):
     return None
 
 
-def roofline_step_ms(T, B, lens, ffn_fused=False):
+def roofline_step_ms(T, B, lens, ffn_fused=False, attn_ln_fused=False):
     """Ideal time of one forward pass: the sum over launches of max(ops / peak, bytes / HBM) with
     algorithmic ops and bytes (weights read once per launch), per kernel kind (ms per step).
-    ffn_fused: the FFN block is one kernel (int8 A, f32 residual and output, no intermediate)."""
+    ffn_fused: the FFN block is one kernel (int8 A, f32 residual and output, no intermediate).
+    attn_ln_fused: the attention output GEMM and LN1 are one kernel (f32 ctx and residual in, the
+    LayerNorm's f32 row, int8 row and scale out; no intermediate)."""
     sum_l2 = float(sum(int(L) * int(L) for L in lens))
     hbm = PEAK_HBM_GBS * 1e9
 
@@ -98,6 +100,10 @@ def roofline_step_ms(T, B, lens, ffn_fused=False):
     }
     for k in (("gemm_ffn_up", "gemm_ffn_down") if ffn_fused else ("ffn_fused",)):
         del per[k]
+    if attn_ln_fused:
+        per["gemm_attn_out"] = 11 * max(2.0 * T * 384 * 384 / (PEAK_INT8_TOPS * 1e12),
+                                        (T * (3 * 384 * 4 + 384 + 8) + 384 * 384 + 384 * 16) / hbm)
+        del per["ln1"]
     return {k: v * 1e3 for k, v in per.items()}
 
 
@@ -272,7 +278,8 @@ def main():
                 "unit": unit, "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom, workload),
                 "avg_launch_us": round(avg_launch_s * 1e6, 2), "algorithmic_per_launch": amount}
     # end-to-end: the sum of every kernel's roofline time against the measured pass
-    roof = roofline_step_ms(T, B, lens, ffn_fused)
+    attn_ln_fused = ktimes["ln1"][1] == 0 and ktimes["gemm_attn_out"][1] > 0
+    roof = roofline_step_ms(T, B, lens, ffn_fused, attn_ln_fused)
     e2e = {"t_roof_ms": round(sum(roof.values()), 4), "t_measured_ms": round(ms_per_step, 4),
            "frac": round(sum(roof.values()) / ms_per_step, 4),
            "per_kernel_frac": {k: round(roof[k] / kernel_ms[k], 4) for k in roof if kernel_ms.get(k)}}

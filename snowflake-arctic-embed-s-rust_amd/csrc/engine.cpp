@@ -360,7 +360,7 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   // an N = 384 GEMM and the LayerNorm of its output: one kernel for few rows
   // (latency-bound), else the two kernels
   auto gemm_then_ln = [&](int gemm_kind, int ln_kind, const GemmArgs& g, int amode, const LnArgs& l) {
-    if (gemm_fuses_ln(g)) {
+    if (gemm_fuses_ln(g, amode)) {
       KernelTimer kt(ws, st, gemm_kind);
       launch_gemm_ln(g, amode, l, st);
       return;

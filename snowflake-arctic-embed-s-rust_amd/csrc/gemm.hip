@@ -384,6 +384,184 @@ __global__ __launch_bounds__(256, 2) void gemm_astat_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Many rows, N = K = 384, f32 A quantized on load with smoothing, residual, and
+// the LayerNorm + SmoothQuant of the output rows: the attention output GEMM and
+// LN1 (reference src/model.rs:695-724: smooth_quantize_row of ctx,
+// gemm_int8_fused(attn_out, residual hidden), then layernorm_smooth_quantize_row,
+// src/simd_math.rs:208-247).
+// A workgroup of 4 waves owns 32 complete rows (wave w: columns 96w..96w+95),
+// so the GEMM's output rows stay in LDS for the LayerNorm instead of going to
+// HBM and back.  The arithmetic is gemm_w8a8_kernel's kAF32QSmooth / kEpiF32
+// and ln_quant_kernel's, in the same order.  ln.dst may alias p.res: a
+// workgroup reads its rows' residuals before it writes their LayerNorm.
+// ---------------------------------------------------------------------------
+constexpr int kLrRows = 32;
+constexpr int kLrPitch = 388;  // LDS floats per row of the output tile
+
+__global__ __launch_bounds__(256, 3) void gemm_ln_rows_kernel(GemmArgs p, LnArgs ln) {
+  constexpr int kCB = 6, kRing = 3, kSteps = 6, NB = 384 / 16;
+  static_assert(kLrRows * kAsPitch <= kLrRows * kLrPitch * 4, "the A tile lives in the row tile's space");
+  // the int8 A tile during the K loop; then the int32 accumulators, the f32
+  // output rows and their squared deviations (3 workgroups fit a CU's LDS)
+  __shared__ __attribute__((aligned(16))) float sT[kLrRows * kLrPitch];
+  int8_t* sA = reinterpret_cast<int8_t*>(sT);
+  __shared__ __attribute__((aligned(16))) float sWs[384], sB[384];
+  __shared__ float s_mean[kLrRows], s_rstd[kLrRows];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fq = lane >> 4;
+  const int m0 = blockIdx.x * kLrRows;
+  // row rl of the tile, float4 columns sub + 8 i (i < 12): the A quantization,
+  // the epilogue and the LayerNorm all use this mapping
+  const int rl = tid >> 3, sub = tid & 7, row = m0 + rl;
+  const bool valid = row < p.M;
+  const int rrow = valid ? row : p.M - 1;
+
+  // loads in the order of use (memory operations retire in order): the A row,
+  // its max, the first kRing K steps of W, w_scale and bias; the residual row
+  // after the K loop
+  const float* xr = reinterpret_cast<const float*>(p.A) + (size_t)rrow * 384;
+  float4 xa[12];
+#pragma unroll
+  for (int i = 0; i < 12; i++) xa[i] = *reinterpret_cast<const float4*>(xr + (sub + 8 * i) * 4);
+  const float amax_a = __uint_as_float(p.a_rowmax[rrow]);
+  const int8_t* wbase = p.w + (size_t)lane * 16;
+  v4i ring[kRing][kCB];
+  auto wload = [&](int kt, v4i (&dst)[kCB]) {
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+      dst[j] = *reinterpret_cast<const v4i*>(wbase + ((size_t)kt * NB + wave * kCB + j) * 1024);
+  };
+#pragma unroll
+  for (int u = 0; u < kRing; u++) wload(u, ring[u]);
+  if (tid < 96) reinterpret_cast<float4*>(sWs)[tid] = reinterpret_cast<const float4*>(p.w_scale)[tid];
+  else if (tid < 192) reinterpret_cast<float4*>(sB)[tid - 96] = reinterpret_cast<const float4*>(p.bias)[tid - 96];
+
+  {  // A quantized as kAF32QSmooth: q = round((x * inv_smooth[j]) * (127 / max_abs))
+    const float inv = 127.0f / amax_a;  // inv_scale = 127.0 / max_abs
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = (sub + 8 * i) * 4;
+      const float4 sm = *reinterpret_cast<const float4*>(p.a_smooth + c);
+      const float4 v = make_float4(xa[i].x * sm.x, xa[i].y * sm.y, xa[i].z * sm.z, xa[i].w * sm.w);
+      *reinterpret_cast<uint32_t*>(&sA[rl * kAsPitch + c]) =
+          pack4(qround(v.x * inv), qround(v.y * inv), qround(v.z * inv), qround(v.w * inv));
+    }
+  }
+  __syncthreads();
+
+  v4i acc[2][kCB];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < kCB; j++) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int kt = 0; kt < kSteps; kt++) {
+    v4i af[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAsPitch + kt * 64 + fq * 16]);
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], ring[kt % kRing][j], acc[i][j], 0, 0, 0);
+    if (kt + kRing < kSteps) wload(kt + kRing, ring[kt % kRing]);
+  }
+  float4 res[12];
+  const float* rr = p.res + (size_t)rrow * 384;
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    const v4i r = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(rr + (sub + 8 * i) * 4));
+    res[i] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z), __int_as_float(r.w));
+  }
+  __syncthreads();  // every wave's K loop is done with the A tile
+  // accumulators into the row tile (lane: rows 16 i + 4 fq + r of column 96 w + 16 j + fr)
+  int* T32 = reinterpret_cast<int*>(sT);
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < kCB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) T32[(i * 16 + fq * 4 + r) * kLrPitch + wave * 96 + j * 16 + fr] = acc[i][j][r];
+  __syncthreads();
+
+  // epilogue: out = fma(f32(acc), sa * ws, bias + res), kept in registers and in the tile
+  const float sa = amax_a / 127.0f;  // scale = max_abs / 127.0
+  float4 xv[12];
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    const int c = (sub + 8 * i) * 4;
+    const int4 a4 = *reinterpret_cast<const int4*>(&T32[rl * kLrPitch + c]);
+    const float4 ws4 = *reinterpret_cast<const float4*>(&sWs[c]);
+    float4 b4 = *reinterpret_cast<const float4*>(&sB[c]);
+    b4.x = b4.x + res[i].x; b4.y = b4.y + res[i].y; b4.z = b4.z + res[i].z; b4.w = b4.w + res[i].w;
+    float4 v;
+    v.x = fmaf((float)a4.x, sa * ws4.x, b4.x);
+    v.y = fmaf((float)a4.y, sa * ws4.y, b4.y);
+    v.z = fmaf((float)a4.z, sa * ws4.z, b4.z);
+    v.w = fmaf((float)a4.w, sa * ws4.w, b4.w);
+    xv[i] = v;
+    *reinterpret_cast<float4*>(&sT[rl * kLrPitch + c]) = v;
+  }
+  __syncthreads();
+
+  // LayerNorm + SmoothQuant of the 32 rows (as ln_quant_kernel): one lane per
+  // row takes the in-order sums, 8 threads per row the rest
+  if (tid < kLrRows) s_mean[tid] = lds_row_sum(&sT[tid * kLrPitch], [](float v) { return v; }) / 384.0f;
+  __syncthreads();
+  const float mean = s_mean[rl];
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    float4 d = xv[i];
+    d.x = d.x - mean; d.y = d.y - mean; d.z = d.z - mean; d.w = d.w - mean;
+    *reinterpret_cast<float4*>(&sT[rl * kLrPitch + (sub + 8 * i) * 4]) = make_float4(d.x * d.x, d.y * d.y, d.z * d.z, d.w * d.w);
+  }
+  __syncthreads();
+  if (tid < kLrRows) {
+    const float var_sum = lds_row_sum(&sT[tid * kLrPitch], [](float v) { return v; });
+    s_rstd[tid] = 1.0f / sqrtf(var_sum / 384.0f + 1e-12f);
+  }
+  __syncthreads();
+  const float rstd = s_rstd[rl];
+  float amax = 0.0f;
+  float4 ys[12];
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    const int c = (sub + 8 * i) * 4;
+    const float4 g = *reinterpret_cast<const float4*>(ln.gamma + c);
+    const float4 b = *reinterpret_cast<const float4*>(ln.beta + c);
+    const float4 sm = *reinterpret_cast<const float4*>(ln.smooth + c);
+    float4 y;
+    y.x = (xv[i].x - mean) * rstd * g.x + b.x;
+    y.y = (xv[i].y - mean) * rstd * g.y + b.y;
+    y.z = (xv[i].z - mean) * rstd * g.z + b.z;
+    y.w = (xv[i].w - mean) * rstd * g.w + b.w;
+    if (valid) *reinterpret_cast<float4*>(ln.dst + (size_t)row * 384 + c) = y;
+    ys[i] = make_float4(y.x * sm.x, y.y * sm.y, y.z * sm.z, y.w * sm.w);
+    amax = nanless_max(amax, fabsf(ys[i].x));
+    amax = nanless_max(amax, fabsf(ys[i].y));
+    amax = nanless_max(amax, fabsf(ys[i].z));
+    amax = nanless_max(amax, fabsf(ys[i].w));
+  }
+  amax = lanes8_max(amax);  // amax is never NaN: fmaxf is nanless_max here
+  const float max_abs = nanless_max(1e-8f, amax);
+  const float inv_scale = 127.0f / max_abs;
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = (sub + 8 * i) * 4;
+      *reinterpret_cast<uint32_t*>(ln.q + (size_t)row * 384 + c) =
+          pack4(qround(ys[i].x * inv_scale), qround(ys[i].y * inv_scale), qround(ys[i].z * inv_scale),
+                qround(ys[i].w * inv_scale));
+    }
+    if (sub == 0) {
+      ln.scale[row] = max_abs / 127.0f;
+      if (ln.rowmax_init) ln.rowmax_init[row] = __float_as_uint(1e-8f);
+      if (ln.rowmax_init2) ln.rowmax_init2[row] = __float_as_uint(1e-8f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small M (latency-bound launches: single sequences, short batches, the
 // layer-11 tail): 16 rows per workgroup of 8 waves.  The workgroup
 // stages its whole A tile (16 x K int8; f32 A is quantized on the way, as astore
@@ -924,7 +1102,11 @@ static void launch_variant(GemmArgs p, hipStream_t st, const LnArgs* ln = nullpt
   hipLaunchKernelGGL((gemm_w8a8_kernel<AM, EM, 48>), dim3(nbase), dim3(256), 0, st, p);
 }
 
-bool gemm_fuses_ln(const GemmArgs& p) { return p.M > 0 && p.N == 384 && small_gemm(p); }
+// the GEMM and the LayerNorm of its output in one kernel: few rows (any A mode,
+// N = 384), or many rows of the attention output GEMM (kAF32QSmooth, N = K = 384)
+bool gemm_fuses_ln(const GemmArgs& p, int amode) {
+  return p.M > 0 && p.N == 384 && (small_gemm(p) || (amode == kAF32QSmooth && p.K == 384 && p.res));
+}
 
 bool gemm_small_path(int m) { return m > 0 && m <= kSmallM; }
 
@@ -948,11 +1130,15 @@ void launch_gemm_pre_ln(const GemmArgs& p, const PreArgs& pre, const LnArgs& ln,
 
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st) {
   if (p.M <= 0) return;
-  if (!gemm_fuses_ln(p)) {  // the GEMM, then the LayerNorm kernel over its output
+  if (!gemm_fuses_ln(p, amode)) {  // the GEMM, then the LayerNorm kernel over its output
     launch_gemm(p, amode, kEpiF32, st);
     LnArgs l = ln;
     l.src = p.out;
     launch_ln_quant(l, kLnSrcF32, st);
+    return;
+  }
+  if (!small_gemm(p)) {  // many rows: kAF32QSmooth, N = K = 384, with residual
+    hipLaunchKernelGGL(gemm_ln_rows_kernel, dim3((p.M + kLrRows - 1) / kLrRows), dim3(256), 0, st, p, ln);
     return;
   }
   if (amode == kAI8) launch_variant<kAI8, kEpiF32>(p, st, &ln);

@@ -94,11 +94,12 @@ void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st);
 // bit 0 of *err when cu[0..B] is not a prefix sum of T with segments of 1..max_len tokens
 void launch_check_segments(const int* cu, int B, int T, int max_len, int* err, hipStream_t st);
 // An N = 384 GEMM (kEpiF32) followed by the LayerNorm + SmoothQuant of its
-// output rows (ln.src is ignored: the GEMM output).  When gemm_fuses_ln(p) (few
-// rows) the LayerNorm runs in the GEMM's epilogue and p.out is not written;
+// output rows (ln.src is ignored: the GEMM output).  When gemm_fuses_ln(p, amode)
+// (few rows, or the many-row attention output GEMM: kAF32QSmooth, K = 384, with
+// residual) the LayerNorm runs in the GEMM's kernel and p.out is not written;
 // otherwise the GEMM writes p.out and launch_ln_quant reads it.
 void launch_gemm_ln(const GemmArgs& p, int amode, const LnArgs& ln, hipStream_t st);
-bool gemm_fuses_ln(const GemmArgs& p);
+bool gemm_fuses_ln(const GemmArgs& p, int amode);
 // Few rows (gemm_small_path): a GEMM whose A operand is the LayerNorm + SmoothQuant
 // of the f32 rows p.A (K = 384) under `ln` (gamma, beta, smooth), applied in each
 // workgroup's prologue; the workgroups of the first column tile also store the

@@ -276,6 +276,23 @@ def test_layer_prefix_state(engine, ws, oracle_model, layers):
     assert np.array_equal(h, rh) and np.array_equal(q, rq) and np.array_equal(sc, rsc)
 
 
+@pytest.mark.parametrize("n,lo,hi,layers", [(8, 300, 512, 1), (10, 400, 512, 2)], ids=["T~3k", "T~4.6k"])
+def test_layer_prefix_state_many_rows(engine, oracle_model, n, lo, hi, layers):
+    """The many-row kernels (past the few-row path's 1,024 rows): the attention output GEMM fused
+    with LN1, the A-stationary or column-tiled QKV, the two-kernel FFN below 4,096 rows and the
+    fused FFN block above; state after `layers` layers bit-exact against the oracle."""
+    seqs = ragged_batch(n, lo, hi, 23 + n)
+    T = sum(len(s) for s in seqs)
+    assert T > 1024
+    w = engine.workspace(T, n)
+    try:
+        h, q, sc = engine.forward_prefix(w, seqs, layers)
+    finally:
+        w.close()
+    rh, rq, rsc = oracle_model.run_prefix(seqs, layers)
+    assert np.array_equal(h, rh) and np.array_equal(q, rq) and np.array_equal(sc, rsc)
+
+
 def test_graph_replay_matches_eager(engine, oracle_model, torch_gpu):
     """Repeated forward passes replay a captured hipGraph: every replay, interleaved with
     eager passes of other shapes and host synchronizations, equals the eager result."""
