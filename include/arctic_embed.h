@@ -265,6 +265,14 @@ int ae_workspace_kernel_times(ae_workspace* ws, double* ms_out, int* counts);
  * (s = smooth_dev, or 1 when NULL) and scale rowmax[m]/127 (rowmax as f32 bits). */
 int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const uint32_t* rowmax_dev,
                           const float* smooth_dev, const float* res_dev, float* out_dev, void* stream);
+/* The attention output projection and LN1 as the forward pass runs them (one
+ * kernel; src/model.rs:695-724): out = the smoothed quantize-on-load GEMM of
+ * ae_debug_gemm_quant_a with residual res_dev (N = K = 384), then dst = the
+ * LayerNorm of out (gamma, beta, eps 1e-12) and q / scale its SmoothQuant int8
+ * rows with ln_smooth_dev.  out itself is not stored; dst may equal res_dev. */
+int ae_debug_gemm_ln(const ae_linear* l, int m, const float* x_dev, const uint32_t* rowmax_dev,
+                     const float* smooth_dev, const float* res_dev, const float* gamma_dev, const float* beta_dev,
+                     const float* ln_smooth_dev, float* dst_dev, int8_t* q_dev, float* scale_dev, void* stream);
 /* int8 A; epilogue g = GELU(out) * g_smooth[n] stored as f32, and
  * rowmax[m] = max(rowmax[m], max_n |g|) on f32 bits (caller pre-sets rowmax). */
 int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,

@@ -85,6 +85,7 @@ _SIGS = {
     "ae_workspace_kernel_times": (_i32, [_vp, _vp, _vp]),
     "ae_debug_gemm_quant_a": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_gemm_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ae_debug_gemm_ln": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ae_debug_ffn": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "ae_parallel_context_create": (_i32, [_vp, _i32, _c.POINTER(_vp)]),
     "ae_parallel_context_destroy": (None, [_vp]),
@@ -407,6 +408,13 @@ class Linear:
     def gemm_quant_a(self, m, x_ptr, rowmax_ptr, smooth_ptr, res_ptr, out_ptr, stream=None):
         """GEMM with A quantized on load from f32 rows (the attn_out / FFN-down variant)."""
         _check(_lib.ae_debug_gemm_quant_a(self._h, int(m), x_ptr, rowmax_ptr, smooth_ptr, res_ptr, out_ptr, stream))
+
+    def gemm_ln(self, m, x_ptr, rowmax_ptr, smooth_ptr, res_ptr, gamma_ptr, beta_ptr, ln_smooth_ptr, dst_ptr, q_ptr,
+                scale_ptr, stream=None):
+        """The attention output GEMM (A quantized on load, smoothed, residual) and the LayerNorm +
+        SmoothQuant of its rows in one kernel; its f32 output is not stored."""
+        _check(_lib.ae_debug_gemm_ln(self._h, int(m), x_ptr, rowmax_ptr, smooth_ptr, res_ptr, gamma_ptr, beta_ptr,
+                                     ln_smooth_ptr, dst_ptr, q_ptr, scale_ptr, stream))
 
     def gemm_gelu(self, m, a_ptr, a_scale_ptr, g_smooth_ptr, out_ptr, rowmax_ptr, stream=None):
         """GEMM with the GELU * smooth epilogue and row absmax (the FFN-up variant)."""

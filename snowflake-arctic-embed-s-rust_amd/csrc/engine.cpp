@@ -1223,6 +1223,38 @@ int ae_debug_gemm_quant_a(const ae_linear* l, int m, const float* x_dev, const u
   return AE_OK;
 }
 
+int ae_debug_gemm_ln(const ae_linear* l, int m, const float* x_dev, const uint32_t* rowmax_dev,
+                     const float* smooth_dev, const float* res_dev, const float* gamma_dev, const float* beta_dev,
+                     const float* ln_smooth_dev, float* dst_dev, int8_t* q_dev, float* scale_dev, void* stream) {
+  if (!l || m <= 0 || !x_dev || !rowmax_dev || !smooth_dev || !res_dev || !gamma_dev || !beta_dev || !ln_smooth_dev ||
+      !dst_dev || !q_dev || !scale_dev)
+    return fail(AE_ERR_INVALID_ARG, "bad arguments");
+  if (l->n != 384 || l->k != 384) return fail(AE_ERR_INVALID_ARG, "ae_debug_gemm_ln: a 384 x 384 linear");
+  aek::GemmArgs p{};
+  p.M = m;
+  p.N = l->n;
+  p.K = l->k;
+  p.A = x_dev;
+  p.a_rowmax = rowmax_dev;
+  p.a_smooth = smooth_dev;
+  p.w = l->w;
+  p.w_scale = l->w_scale;
+  p.bias = l->bias;
+  p.res = res_dev;
+  if (!aek::gemm_fuses_ln(p, aek::kAF32QSmooth)) return fail(AE_ERR_INVALID_ARG, "ae_debug_gemm_ln: not fused");
+  aek::LnArgs ln{};
+  ln.T = m;
+  ln.gamma = gamma_dev;
+  ln.beta = beta_dev;
+  ln.smooth = ln_smooth_dev;
+  ln.dst = dst_dev;
+  ln.q = q_dev;
+  ln.scale = scale_dev;
+  aek::launch_gemm_ln(p, aek::kAF32QSmooth, ln, as_stream(stream));
+  HIP_TRY(hipGetLastError());
+  return AE_OK;
+}
+
 int ae_debug_gemm_gelu(const ae_linear* l, int m, const int8_t* a_dev, const float* a_scale_dev,
                        const float* g_smooth_dev, float* out_dev, uint32_t* rowmax_dev, void* stream) {
   if (!l || m <= 0 || !a_dev || !a_scale_dev || !g_smooth_dev || !out_dev || !rowmax_dev)

@@ -153,6 +153,46 @@ def test_gemm_quantize_on_load_bit_exact(torch_gpu, smooth, n, k):
     assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
 
 
+@pytest.mark.parametrize("m", [37, 1500, 2000])
+def test_gemm_then_layernorm_bit_exact(torch_gpu, m):
+    """The attention output GEMM and LN1 in one kernel (the few-row form at 37 rows, the 32-row
+    many-row form at 1,500 and 2,000 with a partial last tile): f32 LN rows, int8 rows and scales
+    bit for bit against the oracle's smooth_quantize -> gemm_scalar_fused(residual) ->
+    layernorm_smooth_quantize.  Rows include a zero ctx row, a residual row whose mean and variance
+    depend on the summation order (+-1e8 against small values) and a constant output row."""
+    torch = torch_gpu
+    n = k = 384
+    w, ws, b, s = linear_inputs(n, k, 11)
+    rng = np.random.default_rng(m + 5)
+    x = rng.normal(0, 1.5, (m, k)).astype(f32)
+    x[3] = 0.0
+    res = rng.normal(0, 1, (m, n)).astype(f32)
+    res[5, :] = rng.normal(0, 1e-3, n).astype(f32)
+    res[5, 0], res[5, 1] = f32(1e8), f32(-1e8)
+    res[m - 1, :] = f32(2.5)
+    x[m - 1] = 0.0  # output row = bias + 2.5 (constant up to the bias)
+    gamma = (1 + rng.normal(0, 0.05, n)).astype(f32)
+    beta = rng.normal(0, 0.02, n).astype(f32)
+    ln_s = (rng.uniform(0.5, 2.0, n) ** -1).astype(f32)
+    rowmax = np.maximum(np.abs(x * s).max(1), f32(1e-8)).astype(f32)
+    lin = ae.Linear(w, ws, b, s)
+    x_d, rm_d, res_d = dev(torch, x), dev(torch, rowmax.view(np.uint32).astype(np.int32)), dev(torch, res)
+    s_d, g_d, b_d, ls_d = dev(torch, s), dev(torch, gamma), dev(torch, beta), dev(torch, ln_s)
+    dst_d = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    q_d = torch.zeros((m, n), dtype=torch.int8, device="cuda")
+    sc_d = torch.zeros(m, dtype=torch.float32, device="cuda")
+    lin.gemm_ln(m, x_d.data_ptr(), rm_d.data_ptr(), s_d.data_ptr(), res_d.data_ptr(), g_d.data_ptr(), b_d.data_ptr(),
+                ls_d.data_ptr(), dst_d.data_ptr(), q_d.data_ptr(), sc_d.data_ptr())
+    torch.cuda.synchronize()
+    lin.close()
+    q, sc = orc.smooth_quant_rows(x, s)
+    out = orc.gemm(q, sc, w, ws, b, res)
+    ry, rq, rsc = orc.ln_quant_rows(out, gamma, beta, ln_s)
+    assert np.array_equal(bits(dst_d.cpu().numpy()), bits(ry))
+    assert np.array_equal(q_d.cpu().numpy(), rq)
+    assert np.array_equal(bits(sc_d.cpu().numpy()), bits(rsc))
+
+
 @pytest.mark.parametrize("m", [1, 45, 130])
 def test_gemm_gelu_epilogue_bit_exact(torch_gpu, m):
     """FFN-up GEMM with the GELU * inv_smooth epilogue and the row absmax."""
