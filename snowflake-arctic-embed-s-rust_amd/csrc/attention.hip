@@ -120,9 +120,7 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 // The tiles of one (sequence, head) share that head's K and V: with the
 // XCD-contiguous numbering they run on one XCD and hit in its L2.
 // grid: max_tiles * 12 workgroups (a bound); the plan's n tiles give 12 n
-// logical items, item = head * n + tile, numbered XCD-contiguously over the
-// workgroups that the hardware dispatches first, so the surplus workgroups come
-// last on every XCD and leave at once
+// logical items, numbered by plan_item (the surplus workgroups leave at once)
 //
 // kWide: operands in float4 groups with four MFMA results live at a time (one
 // float4 load of K per 16 dims, one float4 LDS read of P per 16 keys, and four
@@ -134,15 +132,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kAttnQ];
   __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
-  const int n_tiles = reinterpret_cast<const int4*>(p.plan)[max_tiles].x;
-  int item;
-  {  // XCD x = blockIdx % 8 takes items [base(x), base(x) + cnt(x)) in dispatch order
-    const int nitems = 12 * n_tiles, q = nitems >> 3, r = nitems & 7;
-    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
-    if (i >= (x < r ? q + 1 : q)) return;  // a surplus workgroup (uniform)
-    item = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
-  }
-  const int h = item / n_tiles, tile = item - h * n_tiles;
+  int h, tile;
+  if (!plan_item(reinterpret_cast<const int4*>(p.plan), max_tiles, h, tile)) return;  // a surplus workgroup
   const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
   const int nq = rec.w;
   if (nq == 0) return;

@@ -163,15 +163,15 @@ __global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const
 }
 
 // One workgroup per (head, tile of 32 queries of one segment), the exact
-// kernel's tile records and XCD-contiguous numbering.  The only LDS tile is the
+// kernel's tile records and numbering (plan_item).  The only LDS tile is the
 // int16 P[32][pitch16] (33 KB at 512 keys): several workgroups per CU.
 __global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles, size_t vt_len) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kSmeQ];
   __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32];
   __shared__ int s_isum[kSmeQ];
-  const int item = xcd_contiguous(blockIdx.x, max_tiles * 12);
-  const int h = item / max_tiles, tile = item - h * max_tiles;
+  int h, tile;
+  if (!plan_item(reinterpret_cast<const int4*>(p.plan), max_tiles, h, tile)) return;  // a surplus workgroup
   const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
   const int nq = rec.w;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;

@@ -255,6 +255,23 @@ __device__ __forceinline__ int xcd_contiguous(int p, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
+// The attention kernels' workgroup numbering over a tile plan whose record
+// max_tiles holds the number n of real tiles (attention_plan_kernel): the 12 n
+// (head, tile) items, item = head * n + tile, are numbered XCD-contiguously over
+// the workgroups the hardware dispatches first (XCD x = id mod 8 takes one
+// contiguous range of items in its dispatch order), so the surplus workgroups of
+// the worst-case grid come last on every XCD.  False for those.
+__device__ __forceinline__ bool plan_item(const int4* plan, int max_tiles, int& h, int& tile) {
+  const int n = plan[max_tiles].x;
+  const int nitems = 12 * n, q = nitems >> 3, r = nitems & 7;
+  const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+  if (i >= (x < r ? q + 1 : q)) return false;
+  const int item = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+  h = item / n;
+  tile = item - h * n;
+  return true;
+}
+
 // index of the segment containing token t: largest b with cu[b] <= t (cu has B+1 entries)
 __device__ __forceinline__ int find_segment(const int* cu, int B, int t) {
   int lo = 0, hi = B - 1;
