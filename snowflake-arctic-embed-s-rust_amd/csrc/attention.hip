@@ -27,55 +27,59 @@ namespace aek {
 // bits), which the attn_out GEMM prologue consumes.
 // ---------------------------------------------------------------------------
 constexpr int kAttnQ = 32;     // queries per workgroup
-// In batches of mostly shorter rows (launch_attention), rows of more than
-// kAttnLongL keys get tiles of kAttnQLong queries, so that the score tile of
-// every tile fits 32 x (kAttnLongL + 4) floats (49.7 KB): three workgroups per CU
-// instead of the two that 32 x 516 floats (66 KB) allow.
-constexpr int kAttnLongL = 384, kAttnQLong = 24;
+// In batches of mostly shorter rows (launch_attention), the tiles of rows of at
+// most kAttnLongL keys and those of longer rows go to two launches: score tiles
+// of at most 32 x (kAttnLongL + 4) floats (49.7 KB, three workgroups per CU) in
+// the first, up to 32 x 516 floats (66 KB, two per CU) in the second.
+constexpr int kAttnLongL = 384;
 
 // Work plan, built on the device from cu_seqlens: one 16-byte record per tile
-// of kAttnQ queries (long_q for rows over kAttnLongL keys), {s0, L, q0, nq} =
-// the segment's first token, its length, the tile's first query and its number
-// of queries, so a workgroup learns its whole assignment from one scalar load.
-// Tiles follow the packed segment order (neighbouring tiles read neighbouring
-// K/V rows); records past the last tile, up to max_tiles, have nq = 0, and
-// record max_tiles holds the number of tiles n in .x.  Rows past lmax (the score
-// row length) get no tiles, and no tile record is written past max_tiles (a
+// of kAttnQ queries, {s0, L, q0, nq} = the segment's first token, its length,
+// the tile's first query and its number of queries, so a workgroup learns its
+// whole assignment from one scalar load.  Tiles follow the packed segment order
+// (neighbouring tiles read neighbouring K/V rows).  A plan holds two lists of
+// max_tiles + 1 records each: the tiles in records 0 .. n - 1 and n in record
+// max_tiles (.x).  split = 0: every tile in list 0; split = 1: rows of at most
+// kAttnLongL keys in list 0, longer rows in list 1.  Rows past lmax (the score
+// row length) get no tiles, and a list holds at most max_tiles tiles (a
 // cu_seqlens that is not a prefix sum of at most T tokens could ask for more).
-__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int max_tiles,
-                                                             int long_q, int4* plan) {
-  __shared__ int part[256];
+__global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int max_tiles, int split,
+                                                             int4* plan) {
+  __shared__ int part[2][256];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
-  int nt = 0;
-  auto qt = [&](int L) { return L > kAttnLongL ? long_q : kAttnQ; };
+  auto list_of = [&](int L) { return split && L > kAttnLongL ? 1 : 0; };
+  int nt[2] = {0, 0};
   for (int b = b0; b < b1; b++) {
     const int L = min(cu[b + 1] - cu[b], lmax);
-    nt += (L + qt(L) - 1) / qt(L);
+    nt[list_of(L)] += (L + kAttnQ - 1) / kAttnQ;
   }
-  part[tid] = nt;
+  part[0][tid] = nt[0];
+  part[1][tid] = nt[1];
   __syncthreads();
-  if (tid == 0) {
+  if (tid < 2) {  // exclusive prefix sums; part[l][0] ends as list l's total (slot 0's prefix is 0)
     int acc = 0;
     for (int i = 0; i < 256; i++) {
-      const int v = part[i];
-      part[i] = acc;
+      const int v = part[tid][i];
+      part[tid][i] = acc;
       acc += v;
     }
-    part[0] = acc;  // slot 0's own prefix is 0 (kept in `at` below)
+    part[tid][0] = acc;
   }
   __syncthreads();
-  const int n = min(part[0], max_tiles);
-  int at = tid == 0 ? 0 : part[tid];
+  int at[2] = {tid == 0 ? 0 : part[0][tid], tid == 0 ? 0 : part[1][tid]};
+  int4* lst[2] = {plan, plan + max_tiles + 1};
+  const int n[2] = {min(part[0][0], max_tiles), min(part[1][0], max_tiles)};
   for (int b = b0; b < b1; b++) {
-    const int s0 = cu[b], L = min(cu[b + 1] - s0, lmax);
-    const int q = qt(L);
-    for (int q0 = 0; q0 < L; q0 += q, at++)
-      if (at < n) plan[at] = make_int4(s0, L, q0, min(q, L - q0));
+    const int s0 = cu[b], L = min(cu[b + 1] - s0, lmax), l = list_of(L);
+    for (int q0 = 0; q0 < L; q0 += kAttnQ, at[l]++)
+      if (at[l] < n[l]) lst[l][at[l]] = make_int4(s0, L, q0, min(kAttnQ, L - q0));
   }
-  for (int t = n + tid; t < max_tiles; t += 256) plan[t] = make_int4(0, 0, 0, 0);
-  if (tid == 0) plan[max_tiles] = make_int4(n, 0, 0, 0);
+  if (tid == 0) {
+    lst[0][max_tiles] = make_int4(n[0], 0, 0, 0);
+    lst[1][max_tiles] = make_int4(n[1], 0, 0, 0);
+  }
 }
 
 // MFMA as an exact multiplier.  v_mfma_f32_16x16x1_4b_f32 with a zero
@@ -114,9 +118,8 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
     for (int i = 0; i < 4; i++) acc[i] = acc[i] + pr[4 * blk + i];
 }
 
-// dynamic LDS: S[rows][pitch] scores -> exps, per tile: pitch = round16(L) + 4,
-// rows = kAttnQ, or long_q for L > kAttnLongL (attention_lds_bytes; long_q is
-// the plan's tile size for such rows)
+// dynamic LDS: S[kAttnQ][pitch] scores -> exps, per tile: pitch = round16(L) + 4
+// (at most the launch's s_pitch, or kAttnLongL + 4 in the short-row launch)
 // The tiles of one (sequence, head) share that head's K and V: with the
 // XCD-contiguous numbering they run on one XCD and hit in its L2.
 // grid: max_tiles * 12 workgroups (a bound); the plan's n tiles give 12 n
@@ -128,20 +131,20 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 // at a time with scalar operands, 92 VGPRs: for short rows, where the score
 // tile leaves room for more waves than the wide variant's registers do.
 template <bool kWide>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles, int long_q) {
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles, int list) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kAttnQ];
   __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
   int h, tile;
-  if (!plan_item(reinterpret_cast<const int4*>(p.plan), max_tiles, h, tile)) return;  // a surplus workgroup
-  const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
+  const int4* plan = reinterpret_cast<const int4*>(p.plan) + (size_t)list * (max_tiles + 1);
+  if (!plan_item(plan, max_tiles, h, tile)) return;  // a surplus workgroup
+  const int4 rec = plan[tile];
   const int nq = rec.w;
   if (nq == 0) return;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;  // L <= s_pitch - 4 (the plan clamps it)
   const int pitch = ((L + 15) & ~15) + 4;        // this tile's score row pitch
-  const int nrows = L > kAttnLongL ? long_q : kAttnQ;  // score rows in LDS (nq <= nrows)
   const int nqh = (nq + 15) >> 4;  // query halves with at least one query
-  float* S = smem;                 // [nrows][pitch]
+  float* S = smem;                 // [kAttnQ][pitch]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: per-wave loop bounds stay scalar
   const int lr = lane & 15, lg = lane >> 4;  // fragment row / block of this lane
@@ -185,8 +188,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   // The dot product starts from its first product instead of 0 + p_0: the two
   // differ only in the sign of a zero sum, and a score's zero sign cannot change
   // expf(s - max) (the row max is then a zero too, or s - max = -max).
-  // (a lane whose row is past nrows, in the second half of a long tile, stores nothing)
-  auto score_half = [&](int t, const float (&kf)[8], const float (&q)[8], float* srow, float& m, bool st) {
+  auto score_half = [&](int t, const float (&kf)[8], const float (&q)[8], float* srow, float& m) {
     float acc[4];
 #pragma unroll
     for (int c = 0; c < 8 / G; c++) {
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     sc.y = acc[1] * kInvSqrtD;
     sc.z = acc[2] * kInvSqrtD;
     sc.w = acc[3] * kInvSqrtD;
-    if (st) *reinterpret_cast<float4*>(srow + t) = sc;  // t + 3 < round16(L) = pitch - 4
+    *reinterpret_cast<float4*>(srow + t) = sc;  // t + 3 < round16(L) = pitch - 4
     // a key t >= L was computed from K row L - 1 (clamped), so its score repeats
     // key L - 1's bit for bit and cannot change the max: no mask needed.  (The
     // narrow layout keeps the masked form: without it the compiler schedules its
@@ -220,12 +222,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
     }
   };
   float* srow0 = &S[lr * pitch];
-  float* srow1 = &S[min(16 + lr, nrows - 1) * pitch];
-  const bool st1 = 16 + lr < nrows;
+  float* srow1 = &S[(16 + lr) * pitch];
   auto score_block = [&](int kb, const float (&kf)[8]) {
     const int t = 16 * kb + 4 * lg;
-    score_half(t, kf, qf[0], srow0, mrow[0], true);
-    if (nqh > 1) score_half(t, kf, qf[1], srow1, mrow[1], st1);  // wave-uniform
+    score_half(t, kf, qf[0], srow0, mrow[0]);
+    if (nqh > 1) score_half(t, kf, qf[1], srow1, mrow[1]);  // wave-uniform
   };
   {
     float ka[8], kb8[8];
@@ -378,7 +379,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tile
   if (has_item) {
     // the output's inv_smooth, loaded ahead of the PV loop
     const float sm = p.rowmax ? p.smooth[h * 32 + 16 * dh + lr] : 0.0f;
-    const float* prow = &S[min(16 * qh + lr, nrows - 1) * pitch];  // rows past nrows: discarded results
+    const float* prow = &S[(16 * qh + lr) * pitch];
     const float inv = s_inv[16 * qh + lr];
     // full groups of 16 keys: no masking.  Group g's V goes to a 4-deep register
     // ring three groups ahead and its P one group ahead (groups 0-2 were loaded
@@ -899,11 +900,7 @@ void launch_mfma_products(const float* a, const float* b, float* out, int n_sets
   if (n_sets > 0) hipLaunchKernelGGL(mfma_products_kernel, dim3(n_sets), dim3(64), 0, st, a, b, out, n_sets);
 }
 
-size_t attention_lds_bytes(int s_pitch, int long_q) {
-  const int max_len = s_pitch - 4;
-  if (max_len <= kAttnLongL) return sizeof(float) * (size_t)kAttnQ * s_pitch;
-  return sizeof(float) * (size_t)max(kAttnQ * (kAttnLongL + 4), long_q * s_pitch);
-}
+size_t attention_lds_bytes(int s_pitch) { return sizeof(float) * (size_t)kAttnQ * s_pitch; }
 
 int attention_pitch(int max_len) {
   const int L = max(1, min(max_len, 512));
@@ -916,7 +913,7 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
 // allow > 64 KiB of dynamic LDS for the tiled kernel on the current device; called
 // at engine open and by the stand-alone operator, never inside a stream capture
 void init_attention_kernels() {
-  const int lds = (int)attention_lds_bytes(attention_pitch(512), kAttnQ);
+  const int lds = (int)attention_lds_bytes(attention_pitch(512));
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<false>),
@@ -931,11 +928,11 @@ void init_attention_kernels() {
 // and latency-bound, run faster with the narrow one's 6.  The choice is by the
 // batch's mean length (both variants give the same bits).
 constexpr int kWideMinMeanLen = 48;
-// mean length up to which rows over kAttnLongL keys get 24-query tiles
-constexpr int kLongTileMaxMean = 320;
+// mean length up to which the rows over kAttnLongL keys get a launch of their own
+constexpr int kSplitMaxMean = 320;
 
-void launch_attention_plan(const AttnArgs& p, hipStream_t st, int long_q, int max_tiles) {
-  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4, max_tiles, long_q,
+void launch_attention_plan(const AttnArgs& p, hipStream_t st, int split, int max_tiles) {
+  hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4, max_tiles, split,
                      reinterpret_cast<int4*>(p.plan));
 }
 
@@ -965,21 +962,27 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
     hipLaunchKernelGGL(attention_rows_kernel<4>, dim3(p.B * 12), dim3(256), 0, st, p);
     return;
   }
-  // 24-query tiles for the rows over kAttnLongL keys only in batches of mostly
-  // shorter rows, by the mean length (the plan, built once per pass, and every
-  // launch of the pass make the same choice): C3's ragged 16-512 batch (mean
-  // 267) 1.5 % faster, C4's rows of 512, where every tile would be a 24-query
-  // one, 7.4 % slower
-  const int long_q = (max_len > kAttnLongL && T <= kLongTileMaxMean * p.B) ? kAttnQLong : kAttnQ;
-  // the grid is sized for the plan's worst case, and an empty workgroup still
-  // costs a record load: without 24-query tiles the bound is T/32 + B + 1
-  const int max_tiles = long_q == kAttnQLong ? attention_max_tiles(p.B, T) : attention_max_tiles32(p.B, T);
-  if (plan) launch_attention_plan(p, st, long_q, max_tiles);
-  const size_t lds = attention_lds_bytes(p.s_pitch, long_q);
-  if (T > kWideMinMeanLen * p.B)
-    hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, long_q);
-  else
-    hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, long_q);
+  // In batches of mostly shorter rows (by the mean length; the plan, built once
+  // per pass, and every launch of the pass make the same choice), the rows over
+  // kAttnLongL keys get a launch of their own, so that the short rows' tiles run
+  // three workgroups per CU.  The grids are sized for the worst case; the
+  // surplus workgroups leave after one scalar load (plan_item).
+  const bool split = max_len > kAttnLongL && T <= kSplitMaxMean * p.B;
+  const int max_tiles = attention_max_tiles(p.B, T);
+  if (plan) launch_attention_plan(p, st, split ? 1 : 0, max_tiles);
+  const bool wide = T > kWideMinMeanLen * p.B;
+  auto launch = [&](int list, size_t lds) {
+    if (wide)
+      hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, list);
+    else
+      hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, list);
+  };
+  if (split) {
+    launch(0, attention_lds_bytes(kAttnLongL + 4));
+    launch(1, attention_lds_bytes(p.s_pitch));
+  } else {
+    launch(0, attention_lds_bytes(p.s_pitch));
+  }
 }
 
 // ---------------------------------------------------------------------------

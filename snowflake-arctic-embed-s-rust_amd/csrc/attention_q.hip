@@ -395,8 +395,8 @@ void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_
   hipLaunchKernelGGL(sme_pack_kernel, dim3((T + 63) / 64), dim3(768), 0, st, p.qkv, p.cu, p.B, T, s);
   const size_t vt_len = sme_vt_len(T, p.B);
   hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
-  const int max_tiles = attention_max_tiles32(p.B, T);  // 32-query tiles only
-  if (plan) launch_attention_plan(p, st, kSmeQ, max_tiles);
+  const int max_tiles = attention_max_tiles(p.B, T);
+  if (plan) launch_attention_plan(p, st, 0, max_tiles);  // every tile in list 0
   hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), sme_p_bytes(p.s_pitch), st, p, s,
                      max_tiles, vt_len);
 }

@@ -1058,9 +1058,9 @@ int ae_attention_varlen_noalloc(const float* qkv_dev, const int32_t* cu_seqlens_
       max_seq_len > ae::kMaxPos)
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments (max_seq_len must be 1..512)");
   if (n_seqs == 0) return AE_OK;
-  if (aek::attention_max_tiles(n_seqs, total_tokens) + 1 > aek::kNoAllocPlanTiles)
-    return fail(AE_ERR_CAPACITY, "ae_attention_varlen_noalloc: total_tokens / 24 + n_seqs + 2 = " +
-                                     std::to_string(aek::attention_max_tiles(n_seqs, total_tokens) + 1) +
+  if (2 * (aek::attention_max_tiles(n_seqs, total_tokens) + 1) > aek::kNoAllocPlanTiles)
+    return fail(AE_ERR_CAPACITY, "ae_attention_varlen_noalloc: 2 (total_tokens / 32 + n_seqs + 2) = " +
+                                     std::to_string(2 * (aek::attention_max_tiles(n_seqs, total_tokens) + 1)) +
                                      " exceeds its static scratch of " + std::to_string(aek::kNoAllocPlanTiles) +
                                      " tiles");
   int* plan = nullptr;

@@ -141,28 +141,24 @@ struct AttnArgs {
   int len1 = 0;            // B == 1 and cu_seqlens = {0, len1} known on the host: the latency form skips its load
 };
 int attention_pitch(int max_len);
-// dynamic LDS of the tiled kernel; long_q: its tile size for rows over 384 keys
-size_t attention_lds_bytes(int s_pitch, int long_q);
-// tiles of 32 queries, 24 for rows of more than 384 keys (the exact kernel's
-// plan): max_tiles >= sum_b ceil(L_b / q_b); T/24 + B + 1 is one
-inline int attention_max_tiles(int B, int T) { return T / 24 + B + 1; }
-// plans of 32-query tiles only (the quantized kernel's)
-inline int attention_max_tiles32(int B, int T) { return T / 32 + B + 1; }
-// ints of `plan` scratch for B segments and T tokens: one 4-int record per tile,
-// and one for the tile count
-inline size_t attention_plan_ints(int B, int T) { return 4 * ((size_t)attention_max_tiles(B, T) + 1); }
+size_t attention_lds_bytes(int s_pitch);
+// tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32); T/32 + B + 1 is one
+inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
+// ints of `plan` scratch for B segments and T tokens: two lists of one 4-int
+// record per tile and one for the list's tile count
+inline size_t attention_plan_ints(int B, int T) { return 8 * ((size_t)attention_max_tiles(B, T) + 1); }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
 // ae_attention_varlen_noalloc: the tile plan in a static device array of this
-// many records (1 MiB), so attention_max_tiles(B, T) + 1 <= kNoAllocPlanTiles
-constexpr int kNoAllocPlanTiles = 65536;
+// many records (2 MiB), so 2 (attention_max_tiles(B, T) + 1) <= kNoAllocPlanTiles
+constexpr int kNoAllocPlanTiles = 131072;
 // the current device's address of that array (resolved on the first call per
 // device, with the device current; not during a stream capture)
 hipError_t noalloc_plan_scratch(int** plan);
 // T = total tokens of the batch; plan = false reuses the plan already in p.plan
 // (launch_attention_plan, which depends only on cu, B and s_pitch)
 void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan = true);
-// long_q: queries per tile for rows of more than 384 keys (32: every tile 32)
-void launch_attention_plan(const AttnArgs& p, hipStream_t st, int long_q, int max_tiles);
+// split = 1: rows of more than 384 keys in the plan's second list
+void launch_attention_plan(const AttnArgs& p, hipStream_t st, int split, int max_tiles);
 // exact-attention kernel choice for later launches: 0 by the batch, 1 tiled /
 // register rows only, 2 the latency form only (a test hook; same bits)
 void set_attention_form(int form);

@@ -342,10 +342,10 @@ def test_gelu_bit_exact_over_float_sample(torch_gpu):
 # exact attention has five code paths, chosen by the batch's shape: the latency
 # form (at most 16 tiles of 32 queries, longest > 64), register-resident rows
 # (longest <= 32, <= 64), else the tiled kernel with the wide (mean > 48) or the
-# narrow operand layout; these length sets reach each.  In the tiled kernel, rows
-# of more than 384 keys have 24-query tiles when the batch's mean length is at
-# most 320 ("tiled_long": both sides of 384, full and partial 24-query tiles,
-# beside short rows in the same launch), else 32-query ones ("tiled_long32")
+# narrow operand layout; these length sets reach each.  The tiled kernel runs the
+# rows of more than 384 keys in a launch of their own when the batch's mean
+# length is at most 320 ("tiled_long": both sides of 384, with short rows), else
+# every row in one launch ("tiled_long32")
 ATTN_LENS = {"tiled_wide": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
              "tiled_long": [384, 385, 17, 408, 409, 431, 1, 449, 480, 500, 511, 512, 24, 25, 200],
              "tiled_long32": [512, 500, 450, 400, 385, 512, 480, 449, 33, 384],
