@@ -750,8 +750,8 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
 
 // Short rows (every sequence of the batch at most 16 * NKB <= 64 keys): one
 // workgroup per (sequence, head), one wave per 16 queries, the whole score row
-// in registers (NKB blocks of 16 keys, 4 scores per lane and block), no LDS tile
-// and no barrier.  Same arithmetic, in the same order, as attention_kernel:
+// in registers (NKB blocks of 16 keys, 4 scores per lane and block).  Same
+// arithmetic, in the same order, as attention_kernel:
 //  * scores: A = K block with its rows permuted so that lane (lg, lr) ends with
 //    query lr and keys 16kb + lg + 4i in result register i, B = Q (dims 4j + b);
 //  * the in-order denominator: each lane gathers the 16 exps of its query and
@@ -760,31 +760,48 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
 //  * PV: MFMA i of block kb multiplies keys 16kb + 4i + j (block j), so register
 //    i is directly its A operand; lane (lg, lr) ends with queries 4lg + r at
 //    dims lr and 16 + lr.
+// The workgroup first stages the segment's Q, K and V rows of the head in LDS
+// with float4 loads (one 128-byte row section per 8 lanes), and the MFMA
+// operands are then read from there: the operands' own layout (4 bytes per
+// lane from 16 rows) read from global memory by every wave kept the address
+// unit busy 90 % of the time.
 // Batches of short sequences spend most of a tiled workgroup on set-up and
-// partial tiles; this form keeps 6 waves per SIMD busy instead.
+// partial tiles; this form keeps 6 workgroups per CU busy instead.
 template <int NKB>
 __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
+  constexpr int kRows = 16 * NKB, kP = 33;  // staged rows; row pitch in floats (conflict-free reads)
+  __shared__ float sQ[kRows * kP], sK[kRows * kP], sV[kRows * kP];
   const int item = xcd_contiguous(blockIdx.x, p.B * 12);
-  const int h = item / p.B, b = item - h * p.B;
+  const int b = item / 12, h = item - b * 12;
   const int s0 = p.cu[b];
-  if (p.skip_from > 0 && p.cu[b + 1] - s0 >= p.skip_from) return;  // another kernel's segment
-  const int L = min(p.cu[b + 1] - s0, 16 * NKB);
+  if (p.skip_from > 0 && p.cu[b + 1] - s0 >= p.skip_from) return;  // another kernel's segment (uniform)
+  const int L = min(p.cu[b + 1] - s0, kRows);
+  {
+    // rows [0, L) of the head's Q, K and V sections: 24 float4s per row
+    const float* src = p.qkv + (size_t)s0 * HQKV + h * 32;
+    for (int c = threadIdx.x; c < 24 * L; c += blockDim.x) {
+      const int r = c / 24, w = c - 24 * r, sec = w >> 3, f = 4 * (w & 7);
+      const float4 v = *reinterpret_cast<const float4*>(src + (size_t)r * HQKV + sec * H + f);
+      float* dst = (sec == 0 ? sQ : sec == 1 ? sK : sV) + r * kP + f;
+      dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
+  }
+  __syncthreads();
   const int lane = threadIdx.x & 63, q0 = (threadIdx.x >> 6) * 16;
   if (q0 >= L) return;  // wave-uniform; nothing below synchronizes across waves
   const int lr = lane & 15, lg = lane >> 4;
   const ExpTab tb = exp_tab_regs();
-  const float* qkv = p.qkv + (size_t)s0 * HQKV + h * 32;
   const int nkb = (L + 15) >> 4;
 
   float qf[8];
   {
-    const float* qrow = qkv + (size_t)min(q0 + lr, L - 1) * HQKV;
+    const float* qrow = sQ + min(q0 + lr, L - 1) * kP + lg;
 #pragma unroll
-    for (int j = 0; j < 8; j++) qf[j] = qrow[4 * j + lg];
+    for (int j = 0; j < 8; j++) qf[j] = qrow[4 * j];
   }
   const int kperm = 4 * (lr & 3) + (lr >> 2);  // key of A row lr within a block
   auto load_kf = [&](int kb, float (&kf)[8]) {
-    const float* src = qkv + H + lg + (size_t)min(16 * kb + kperm, L - 1) * HQKV;
+    const float* src = sK + min(16 * kb + kperm, L - 1) * kP + lg;
 #pragma unroll
     for (int j = 0; j < 8; j++) kf[j] = src[4 * j];
   };
@@ -842,7 +859,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
   auto load_vf = [&](int kb, float (&vf)[2][4]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float* src = qkv + 2 * H + lr + (size_t)min(16 * kb + 4 * i + lg, L - 1) * HQKV;
+      const float* src = sV + min(16 * kb + 4 * i + lg, L - 1) * kP + lr;
       vf[0][i] = src[0];
       vf[1][i] = src[16];
     }
