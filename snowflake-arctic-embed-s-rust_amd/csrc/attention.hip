@@ -760,29 +760,30 @@ __global__ __launch_bounds__(512) void attention_lat_kernel(AttnArgs p, int tile
 //  * PV: MFMA i of block kb multiplies keys 16kb + 4i + j (block j), so register
 //    i is directly its A operand; lane (lg, lr) ends with queries 4lg + r at
 //    dims lr and 16 + lr.
-// The workgroup first stages the segment's Q, K and V rows of the head in LDS
+// The workgroup first stages the segment's K and V rows of the head in LDS
 // with float4 loads (one 128-byte row section per 8 lanes), and the MFMA
 // operands are then read from there: the operands' own layout (4 bytes per
 // lane from 16 rows) read from global memory by every wave kept the address
-// unit busy 90 % of the time.
+// unit busy 90 % of the time.  (Each wave still loads its own Q operands, once:
+// without a Q tile the LDS admits 8 workgroups per CU, as the 64 registers do.)
 // Batches of short sequences spend most of a tiled workgroup on set-up and
-// partial tiles; this form keeps 6 workgroups per CU busy instead.
+// partial tiles; this form keeps 8 waves per SIMD busy instead.
 template <int NKB>
-__global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
+__global__ __launch_bounds__(256, 8) void attention_rows_kernel(AttnArgs p) {
   constexpr int kRows = 16 * NKB, kP = 33;  // staged rows; row pitch in floats (conflict-free reads)
-  __shared__ float sQ[kRows * kP], sK[kRows * kP], sV[kRows * kP];
+  __shared__ float sK[kRows * kP], sV[kRows * kP];
   const int item = xcd_contiguous(blockIdx.x, p.B * 12);
   const int b = item / 12, h = item - b * 12;
   const int s0 = p.cu[b];
   if (p.skip_from > 0 && p.cu[b + 1] - s0 >= p.skip_from) return;  // another kernel's segment (uniform)
   const int L = min(p.cu[b + 1] - s0, kRows);
   {
-    // rows [0, L) of the head's Q, K and V sections: 24 float4s per row
-    const float* src = p.qkv + (size_t)s0 * HQKV + h * 32;
-    for (int c = threadIdx.x; c < 24 * L; c += blockDim.x) {
-      const int r = c / 24, w = c - 24 * r, sec = w >> 3, f = 4 * (w & 7);
+    // rows [0, L) of the head's K and V sections: 16 float4s per row
+    const float* src = p.qkv + (size_t)s0 * HQKV + H + h * 32;
+    for (int c = threadIdx.x; c < 16 * L; c += blockDim.x) {
+      const int r = c >> 4, sec = (c >> 3) & 1, f = 4 * (c & 7);
       const float4 v = *reinterpret_cast<const float4*>(src + (size_t)r * HQKV + sec * H + f);
-      float* dst = (sec == 0 ? sQ : sec == 1 ? sK : sV) + r * kP + f;
+      float* dst = (sec == 0 ? sK : sV) + r * kP + f;
       dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
     }
   }
@@ -795,7 +796,7 @@ __global__ __launch_bounds__(256) void attention_rows_kernel(AttnArgs p) {
 
   float qf[8];
   {
-    const float* qrow = sQ + min(q0 + lr, L - 1) * kP + lg;
+    const float* qrow = p.qkv + (size_t)(s0 + min(q0 + lr, L - 1)) * HQKV + h * 32 + lg;
 #pragma unroll
     for (int j = 0; j < 8; j++) qf[j] = qrow[4 * j];
   }
