@@ -1233,8 +1233,160 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   }
 }
 
+// The same for batches whose segments are at most 64 tokens long: one wave per
+// (sequence, head), lane t holding key t, four heads per workgroup (grid B x 3),
+// the same arithmetic in the same order as cls_attention_kernel.  With a
+// workgroup per (sequence, head), three of its four waves had no key in most
+// phases, and the launch was bound by the latency of its ~100 k workgroups.
+__global__ __launch_bounds__(256, 6) void cls_attention_short_kernel(ClsArgs p) {
+  __shared__ __attribute__((aligned(16))) float S[4][64];
+  __shared__ __attribute__((aligned(16))) float sQ[4][32];
+  const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = 4 * blockIdx.y + wave;
+  const int s0 = p.cu[b], L = min(p.cu[b + 1] - s0, min(p.max_len, 64));
+  const ExpTab tb = exp_tab_regs();
+  // q_only for the [CLS] row and this head's 32 columns (as cls_attention_kernel)
+  v4i qa[6], qb[6][2];
+#pragma unroll
+  for (int kt = 0; kt < 6; kt++) {
+    qa[kt] = (lane & 15) == 0 ? *reinterpret_cast<const v4i*>(p.act_q + (size_t)s0 * H + kt * 64 + (lane >> 4) * 16)
+                              : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      qb[kt][j] = *reinterpret_cast<const v4i*>(p.wq + (((size_t)kt * (H / 16) + 2 * h + j) * 64 + lane) * 16);
+  }
+  float4 kr[8];
+  {
+    v4i acc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+    for (int kt = 0; kt < 6; kt++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[kt], qb[kt][j], acc[j], 0, 0, 0);
+    // the K row of key `lane`, loaded once the MFMA operands' registers are free
+    // (loaded with them, the three sets held 104 registers: 4 waves per SIMD)
+    if (lane < L) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) kr[e] = *reinterpret_cast<const float4*>(p.kv + (size_t)(s0 + lane) * 2 * H + h * 32 + 4 * e);
+    }
+    if (lane < 16) {  // row 0 of the result: lane l holds columns 16 j + l, register 0
+      const float sa = p.act_scale[s0];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int col = h * 32 + 16 * j + lane;
+        sQ[wave][16 * j + lane] = fmaf((float)acc[j][0], sa * p.wq_scale[col], p.wq_bias[col]);
+      }
+    }
+  }
+  wave_lds_sync();
+  // the PV lanes' first V values (keys 0-15, dim `lane`; rows past the segment
+  // clamped), issued now so that their latency hides behind the softmax
+  const float* vcol = p.kv + (size_t)s0 * 2 * H + H + h * 32 + (lane & 31);
+  const int nvb = L >> 3;  // full batches of 8 keys
+  float va[8], vb[8];
+  auto ldv = [&](int bi, float (&v)[8]) {
+    const int t0 = 8 * min(bi, max(nvb - 1, 0));
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = vcol[(size_t)min(t0 + k, L - 1) * 2 * H];
+  };
+  if (L > 0) {
+    ldv(0, va);
+    ldv(1, vb);
+  }
+  // score of key `lane` (dot32_f32 order) and the max over the keys
+  float sc = 0.0f, m = -INFINITY;
+  if (lane < L) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {  // q read as needed (an LDS broadcast), not held in 32 registers
+      const float4 q = *reinterpret_cast<const float4*>(&sQ[wave][4 * e]);
+      sum += q.x * kr[e].x;
+      sum += q.y * kr[e].y;
+      sum += q.z * kr[e].z;
+      sum += q.w * kr[e].w;
+    }
+    sc = sum * kInvSqrtD;
+    m = nanless_max(m, sc);  // a NaN score is never the max (the reference's `if s > max`)
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) m = nanless_max(m, __shfl_xor(m, off, 64));
+  const float e = expf_libm(sc - m, tb);  // all lanes (expf_libm); keys past L unused
+  if (lane < L) S[wave][lane] = e;
+  wave_lds_sync();
+  float inv = 0.0f;
+  if (lane == 0) {  // in-order denominator, 16-key batches read ahead of their adds
+    float sum = 0.0f;
+    const int nb = L >> 4;
+    float4 ea[4], eb[4];
+    auto ld = [&](int bi, float4 (&v)[4]) {
+      const float4* src = reinterpret_cast<const float4*>(&S[wave][16 * min(bi, nb - 1)]);
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = src[i];
+    };
+    auto add = [&](const float4 (&v)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sum += v[i].x; sum += v[i].y; sum += v[i].z; sum += v[i].w;
+      }
+    };
+    if (nb > 0) {
+      ld(0, ea);
+      int bi = 0;
+      for (; bi + 2 <= nb; bi += 2) {
+        ld(bi + 1, eb);
+        __builtin_amdgcn_sched_barrier(0);
+        add(ea);
+        __builtin_amdgcn_sched_barrier(0);
+        ld(bi + 2, ea);
+        __builtin_amdgcn_sched_barrier(0);
+        add(eb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (bi < nb) add(ea);
+    }
+    for (int j = 16 * nb; j < L; j++) sum += S[wave][j];
+    inv = 1.0f / sum;
+  }
+  inv = __shfl(inv, 0, 64);
+  if (lane < L) S[wave][lane] = e * inv;
+  wave_lds_sync();
+  float o = 0.0f;
+  if (lane < 32) {  // ctx_d = sum_t p_t * v_t,d in order; V two batches of 8 keys ahead
+    auto add = [&](int bi, const float (&v)[8]) {
+      const float4 p0 = *reinterpret_cast<const float4*>(&S[wave][8 * bi]);
+      const float4 p1 = *reinterpret_cast<const float4*>(&S[wave][8 * bi + 4]);
+      o = o + p0.x * v[0];
+      o = o + p0.y * v[1];
+      o = o + p0.z * v[2];
+      o = o + p0.w * v[3];
+      o = o + p1.x * v[4];
+      o = o + p1.y * v[5];
+      o = o + p1.z * v[6];
+      o = o + p1.w * v[7];
+    };
+    int bi = 0;
+    for (; bi + 2 <= nvb; bi += 2) {  // va holds batch bi, vb batch bi + 1
+      add(bi, va);
+      ldv(bi + 2, va);
+      add(bi + 1, vb);
+      ldv(bi + 3, vb);
+    }
+    if (bi < nvb) add(bi, va);
+    for (int t = 8 * nvb; t < L; t++) o = o + S[wave][t] * vcol[(size_t)t * 2 * H];
+    p.ctx_c[(size_t)b * H + h * 32 + lane] = o;
+  }
+  float a = lane < 32 ? fabsf(o * p.smooth[h * 32 + lane]) : 0.0f;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
+  if (lane == 0) atomicMax(&p.rowmax_ctx_c[b], __float_as_uint(a));
+  if (h == 0)  // gather the [CLS] row of hidden (the tail's residual), last: no registers held meanwhile
+    for (int i = lane; i < 96; i += 64)
+      reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[i] = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[i];
+}
+
 void launch_cls(const ClsArgs& p, hipStream_t st) {
-  hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), 0, st, p);
+  if (p.max_len <= 64)
+    hipLaunchKernelGGL(cls_attention_short_kernel, dim3(p.B, 3), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(cls_attention_kernel, dim3(p.B, 12), dim3(256), 0, st, p);
 }
 
 }  // namespace aek
