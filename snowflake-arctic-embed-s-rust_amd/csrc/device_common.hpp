@@ -24,13 +24,15 @@ constexpr float kInvSqrtD = 0.17677669529663687f;  // 1.0f / sqrtf(32.0f), src/m
 // ---------------------------------------------------------------------------
 
 // `(v).round().clamp(-127.0, 127.0) as i8` (f32::round = half away from zero;
-// `as i8` maps NaN to 0), as trunc(|v| + (0.5 - 2^-25)) with v's sign, then
-// v_cvt_i32_f32 (saturating, NaN -> 0) and the clamp: the sum rounds up to the
-// next integer exactly when |v| has a fraction >= 0.5.  Equal to the
-// roundf / NaN test / clamp form on all 2^32 inputs (exhaustive CPU check with
-// the conversion's saturation), in five instructions instead of about ten.
+// `as i8` maps NaN to 0), as the truncating, saturating v_cvt_i32_f32 (NaN -> 0)
+// of v + (0.5 - 2^-25) with v's sign, then the clamp: |v| + (0.5 - 2^-25) rounds
+// up to the next integer exactly when |v| has a fraction >= 0.5, and a
+// round-to-nearest-even sum is odd under negation, so adding the signed
+// constant and truncating equals trunc(|v| + 0.5 - 2^-25) with v's sign.  Equal
+// to the roundf / NaN test / clamp form on all 2^32 inputs (exhaustive CPU check
+// with the conversion's saturation), in four instructions.
 __device__ __forceinline__ int qround(float v) {
-  const float r = copysignf(__builtin_truncf(fabsf(v) + 0x1.fffffep-2f), v);
+  const float r = v + copysignf(0x1.fffffep-2f, v);
   int q;
   asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
   return max(-127, min(q, 127));
@@ -38,14 +40,13 @@ __device__ __forceinline__ int qround(float v) {
 
 // qround for |x| <= 127.5 or NaN, which holds wherever x = v * (127 / max_abs)
 // with max_abs >= |v| (|x| <= 127 * (1 + 2^-24)^2 after the two roundings):
-// round half away from zero as trunc(|x| + (0.5 - 2^-25)) with x's sign.  That
-// sum rounds up to the next integer exactly when |x| has a fraction >= 0.5: equal
-// to roundf on all 1.12 G non-negative floats up to 127.5 (exhaustive CPU check).
-// The clamp to [-127, 127] cannot bind in that range; v_cvt_i32_f32 maps NaN to
-// 0, as the reference's `as i8` does (inline asm: a C++ float-to-int cast of NaN
-// would be undefined).
+// round half away from zero as the truncating convert of x + (0.5 - 2^-25) with
+// x's sign (as qround; equal to roundf on all 2.26 G such floats, exhaustive CPU
+// check).  The clamp to [-127, 127] cannot bind in that range; v_cvt_i32_f32
+// maps NaN to 0, as the reference's `as i8` does (inline asm: a C++
+// float-to-int cast of NaN would be undefined).
 __device__ __forceinline__ int qround_bounded(float x) {
-  const float r = copysignf(__builtin_truncf(fabsf(x) + 0x1.fffffep-2f), x);
+  const float r = x + copysignf(0x1.fffffep-2f, x);
   int q;
   asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
   return q;
