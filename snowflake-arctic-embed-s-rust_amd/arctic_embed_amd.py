@@ -78,6 +78,7 @@ _SIGS = {
     "ae_debug_gelu_map": (_i32, [_vp, _vp, _sz, _vp]),
     "ae_debug_mfma_products": (_i32, [_vp, _vp, _vp, ctypes.c_int, _vp]),
     "ae_debug_set_attention_form": (_i32, [ctypes.c_int]),
+    "ae_debug_set_ffn_rows": (_i32, [ctypes.c_int]),
     "ae_workspace_set_timing": (_i32, [_vp, _i32]),
     "ae_workspace_set_graphs": (_i32, [_vp, _i32]),
     "ae_workspace_set_attention_mode": (_i32, [_vp, _i32]),
@@ -478,3 +479,9 @@ def set_attention_form(form):
     """Exact-attention kernels to launch from now on: 0 by the batch (default),
     1 tiled / register rows only, 2 the latency form only (a test hook)."""
     _check(_lib.ae_debug_set_attention_form(int(form)))
+
+
+def set_ffn_rows(rows):
+    """Token rows per workgroup of the fused FFN kernel from now on: 0 by the
+    batch (default), 32 or 64 (a test hook)."""
+    _check(_lib.ae_debug_set_ffn_rows(int(rows)))

@@ -1326,6 +1326,13 @@ int ae_debug_set_attention_form(int form) {
   return AE_OK;
 }
 
+// test hook: the FFN kernel's workgroup height
+int ae_debug_set_ffn_rows(int rows) {
+  if (rows != 0 && rows != 32 && rows != 64) return fail(AE_ERR_INVALID_ARG, "FFN rows must be 0, 32 or 64");
+  aek::set_ffn_rows(rows);
+  return AE_OK;
+}
+
 int ae_debug_mfma_products(const float* a_dev, const float* b_dev, float* out_dev, int n_sets, void* stream) {
   if (!a_dev || !b_dev || !out_dev || n_sets < 0) return fail(AE_ERR_INVALID_ARG, "bad mfma_products arguments");
   aek::launch_mfma_products(a_dev, b_dev, out_dev, n_sets, as_stream(stream));

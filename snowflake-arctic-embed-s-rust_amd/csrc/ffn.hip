@@ -50,20 +50,33 @@ __device__ __forceinline__ uint32_t quad_transpose_bytes(uint32_t v, int k) {
 }
 }  // namespace
 
+// kP passes of 32 rows per workgroup (kP = 2: 64 rows): each pass runs FFN-up,
+// its GELU, the row absmax and the quantization into rows [32 pp, 32 pp + 32) of
+// the LDS intermediate; FFN-down then streams W2 once for all 32 kP rows (590 KB
+// per workgroup through the CU's vector memory path, the phase's bound).  Pass
+// pp + 1's input rows are staged with pass pp's, and its first weight fragments
+// are loaded after pass pp's GELU loop.
+template <int kP>
 __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
-  __shared__ __attribute__((aligned(16))) int8_t sA[kRows * kAPitch];
-  __shared__ __attribute__((aligned(16))) int8_t sQ[kRows * kQPitch];
-  __shared__ __attribute__((aligned(16))) float sMax[kRows][kWaves];  // per-wave row absmax of g
-  __shared__ __attribute__((aligned(16))) int sE[kWaves][kRows * kEPitch];
+  constexpr int kT = kRows * kP;  // token rows per workgroup
+  __shared__ __attribute__((aligned(16))) int8_t sA[kP][kRows * kAPitch];
+  __shared__ __attribute__((aligned(16))) int8_t sQ[kT * kQPitch];
+  __shared__ __attribute__((aligned(16))) float sMax[kT][kWaves];  // per-wave row absmax of g
+  // the FFN-down epilogue's per-wave staging tiles (kRows rows at a time): their
+  // own array at kP = 1, the intermediate's space at kP = 2 (free once FFN-down
+  // has read it; 53 KB of 99 KB)
+  constexpr int kEWords = kRows * kEPitch;
+  __shared__ __attribute__((aligned(16))) int sE1[kP == 1 ? kWaves * kEWords : 4];
+  static_assert(kP == 1 || (size_t)kWaves * kEWords * 4 <= sizeof(sQ), "staging fits the intermediate");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fq = lane >> 4;  // MFMA: operand row / output column; k group / output row quad
-  const int m0 = blockIdx.x * kRows;
+  const int m0 = blockIdx.x * kT;
 
-  // input tile: 32 rows x 384 int8 (rows past M repeat row M-1; never stored)
-  for (int c = tid; c < kRows * (kH / 16); c += 512) {
+  // input tiles: kP x 32 rows x 384 int8 (rows past M repeat row M-1; never stored)
+  for (int c = tid; c < kT * (kH / 16); c += 512) {
     const int row = c / (kH / 16), c16 = c - row * (kH / 16);
     const int grow = min(m0 + row, p.M - 1);
-    *reinterpret_cast<v4i*>(&sA[row * kAPitch + c16 * 16]) =
+    *reinterpret_cast<v4i*>(&sA[row / kRows][(row % kRows) * kAPitch + c16 * 16]) =
         __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.A + (size_t)grow * kH + c16 * 16));
   }
 
@@ -80,100 +93,128 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
       dst[kt] = *reinterpret_cast<const v4i*>(w1 + ((size_t)kt * (kF / 16) + cb1 + j) * 1024);
   };
   v4i acc[2][kUpCB];
-  auto mma_col = [&](int j, const v4i* bf) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) acc[i][j] = v4i{0, 0, 0, 0};
-#pragma unroll
-    for (int kt = 0; kt < kUpSteps; kt++) {
-      v4i af[2];
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-        af[i] = *reinterpret_cast<const v4i*>(&sA[(i * 16 + fr) * kAPitch + kt * 64 + fq * 16]);
-#pragma unroll
-      for (int i = 0; i < 2; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt], acc[i][j], 0, 0, 0);
-    }
-  };
   v4i bq[2][kUpSteps];  // fragments of column blocks j + 1 (then j + 3) and j + 2
   load_col(0, bq[0]);
   load_col(1, bq[1]);
-  __syncthreads();  // the input tile is in LDS
-  mma_col(0, bq[0]);
-  load_col(2, bq[0]);
-
-  // GELU epilogue: g = GELU(fma(f32(acc), sa*ws, b)) * inv_smooth, in place.
-  // This lane holds rows 16i + 4fq + r (i < 2, r < 4) of column (cb1 + j)*16 + fr.
-  float sa[2][4], mx[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      sa[i][r] = p.a_scale[min(m0 + i * 16 + fq * 4 + r, p.M - 1)];
-      mx[i][r] = 1e-8f;  // max_abs starts at 1e-8 (src/simd_math.rs:1295-1312)
-    }
-  const ExpTab tb = exp_tab_regs();  // wave-uniform from here to the end of the loop
-#pragma unroll
-  for (int j = 0; j < kUpCB; j++) {
-    // waves w and w + 4 share a SIMD; alternating their priority per column block
-    // keeps them level, so neither waits long at the barrier after the loop
-    if ((j ^ (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
-    else __builtin_amdgcn_s_setprio(0);
-    if (j + 1 < kUpCB) {
-      mma_col(j + 1, bq[(j + 1) & 1]);
-      if (j + 3 < kUpCB) load_col(j + 3, bq[(j + 1) & 1]);
-    }
-    const int col = (cb1 + j) * 16 + fr;
-    const float ws = p.w1_scale[col], bb = p.b1[col], gs = p.g_smooth[col];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float v = fmaf((float)acc[i][j][r], sa[i][r] * ws, bb);
-        float g = gelu_exact(v, tb) * gs;
-        // g is materialized here, in program order: without this the compiler
-        // sinks the GELU tails towards their later uses and keeps every
-        // head's double-precision temporaries live (hundreds of spills)
-        asm volatile("" : "+v"(g));
-        acc[i][j][r] = __float_as_int(g);
-        mx[i][r] = nanless_max(mx[i][r], fabsf(g));
-      }
-  }
-  __builtin_amdgcn_s_setprio(0);
-  // row absmax: over the 16 lanes of this row quad (no NaN: nanless_max above),
-  // then over the 8 waves via LDS
-#pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) mx[i][r] = row16_max(mx[i][r]);
-  if (fr == 0) {
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) sMax[i * 16 + fq * 4 + r][wave] = mx[i][r];
-  }
-  __syncthreads();
+  const ExpTab tb = exp_tab_regs();  // wave-uniform from here to the end of the GELU loops
   auto row_absmax = [&](int row) {
     const float4 a = *reinterpret_cast<const float4*>(&sMax[row][0]);
     const float4 b = *reinterpret_cast<const float4*>(&sMax[row][4]);
     return fmaxf(fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w)), fmaxf(fmaxf(b.x, b.y), fmaxf(b.z, b.w)));
   };
+  // this lane's row scales (rows 16i + 4fq + r of a pass), the next pass's loaded
+  // at the end of this pass's GELU loop
+  float sa[2][4], sa_next[2][4];
+  auto load_sa = [&](int r0, float (&dst)[2][4]) {
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) dst[i][r] = p.a_scale[min(m0 + r0 + i * 16 + fq * 4 + r, p.M - 1)];
+  };
+  load_sa(0, sa);
+  __syncthreads();  // the input tiles are in LDS
+#pragma unroll
+  for (int pp = 0; pp < kP; pp++) {
+    const int8_t* sAp = sA[pp];
+    const int r0 = kRows * pp;  // this pass's first row in the tile
+    // the per-column operands are loaded again in every pass: opaque copies of
+    // their pointers keep the compiler from hoisting the 36 loads out of the
+    // pass loop (and holding 36 more registers through the GELUs)
+    const float *w1s = p.w1_scale, *b1 = p.b1, *gsm = p.g_smooth;
+    asm volatile("" : "+s"(w1s), "+s"(b1), "+s"(gsm));
+    auto mma_col = [&](int j, const v4i* bf) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int kt = 0; kt < kUpSteps; kt++) {
+        v4i af[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+          af[i] = *reinterpret_cast<const v4i*>(&sAp[(i * 16 + fr) * kAPitch + kt * 64 + fq * 16]);
+#pragma unroll
+        for (int i = 0; i < 2; i++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[kt], acc[i][j], 0, 0, 0);
+      }
+    };
+    mma_col(0, bq[0]);
+    load_col(2, bq[0]);
 
-  // ---- quantize: q = round(g * (127 / max_abs)) into the LDS tile ----
-  // A lane's 4 values of one tile are 4 rows of one column; a quad byte
-  // transpose turns them into 4 columns of one row, written as one dword.
-  const int qk = fr & 3;
+    // GELU epilogue: g = GELU(fma(f32(acc), sa*ws, b)) * inv_smooth, in place.
+    // This lane holds rows r0 + 16i + 4fq + r (i < 2, r < 4) of column (cb1 + j)*16 + fr.
+    float mx[2][4];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    float inv_scale[4];
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) inv_scale[r] = 127.0f / row_absmax(i * 16 + fq * 4 + r);
-    int8_t* dst = &sQ[(i * 16 + fq * 4 + qk) * kQPitch + cb1 * 16 + (fr & 12)];
+      for (int r = 0; r < 4; r++) mx[i][r] = 1e-8f;  // max_abs starts at 1e-8 (src/simd_math.rs:1295-1312)
 #pragma unroll
     for (int j = 0; j < kUpCB; j++) {
-      const uint32_t col4 = pack4(qround_bounded(__int_as_float(acc[i][j][0]) * inv_scale[0]),
-                                  qround_bounded(__int_as_float(acc[i][j][1]) * inv_scale[1]),
-                                  qround_bounded(__int_as_float(acc[i][j][2]) * inv_scale[2]),
-                                  qround_bounded(__int_as_float(acc[i][j][3]) * inv_scale[3]));
-      *reinterpret_cast<uint32_t*>(dst + j * 16) = quad_transpose_bytes(col4, qk);
+      // waves w and w + 4 share a SIMD; alternating their priority per column block
+      // keeps them level, so neither waits long at the barrier after the loop
+      if ((j ^ (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+      if (j + 1 < kUpCB) {
+        mma_col(j + 1, bq[(j + 1) & 1]);
+        if (j + 3 < kUpCB) load_col(j + 3, bq[(j + 1) & 1]);
+      }
+      const int col = (cb1 + j) * 16 + fr;
+      const float ws = w1s[col], bb = b1[col], gs = gsm[col];
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float v = fmaf((float)acc[i][j][r], sa[i][r] * ws, bb);
+          float g = gelu_exact(v, tb) * gs;
+          // g is materialized here, in program order: without this the compiler
+          // sinks the GELU tails towards their later uses and keeps every
+          // head's double-precision temporaries live (hundreds of spills)
+          asm volatile("" : "+v"(g));
+          acc[i][j][r] = __float_as_int(g);
+          mx[i][r] = nanless_max(mx[i][r], fabsf(g));
+        }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    if (pp + 1 < kP) {  // the next pass's first weight blocks and row scales, behind the absmax and quantization
+      load_col(0, bq[0]);
+      load_col(1, bq[1]);
+      load_sa(r0 + kRows, sa_next);
+    }
+    // row absmax: over the 16 lanes of this row quad (no NaN: nanless_max above),
+    // then over the 8 waves via LDS
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) mx[i][r] = row16_max(mx[i][r]);
+    if (fr == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sMax[r0 + i * 16 + fq * 4 + r][wave] = mx[i][r];
+    }
+    __syncthreads();
+
+    // ---- quantize: q = round(g * (127 / max_abs)) into the LDS tile ----
+    // A lane's 4 values of one tile are 4 rows of one column; a quad byte
+    // transpose turns them into 4 columns of one row, written as one dword.
+    const int qk = fr & 3;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      float inv_scale[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) inv_scale[r] = 127.0f / row_absmax(r0 + i * 16 + fq * 4 + r);
+      int8_t* dst = &sQ[(r0 + i * 16 + fq * 4 + qk) * kQPitch + cb1 * 16 + (fr & 12)];
+#pragma unroll
+      for (int j = 0; j < kUpCB; j++) {
+        const uint32_t col4 = pack4(qround_bounded(__int_as_float(acc[i][j][0]) * inv_scale[0]),
+                                    qround_bounded(__int_as_float(acc[i][j][1]) * inv_scale[1]),
+                                    qround_bounded(__int_as_float(acc[i][j][2]) * inv_scale[2]),
+                                    qround_bounded(__int_as_float(acc[i][j][3]) * inv_scale[3]));
+        *reinterpret_cast<uint32_t*>(dst + j * 16) = quad_transpose_bytes(col4, qk);
+      }
+    }
+    if (pp + 1 < kP) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sa[i][r] = sa_next[i][r];
     }
   }
 
@@ -190,69 +231,94 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
   for (int s = 0; s < kRing; s++) load_b2(s, ring[s]);
   // the epilogue's residual float4s, loaded now so that HBM latency hides behind FFN-down
   constexpr int kF4 = kDnCB * 4;              // float4 columns of one wave row (12)
-  constexpr int kEpiIt = kRows * kF4 / 64;    // float4s per lane (6)
+  constexpr int kEpiIt = kRows * kF4 / 64;    // float4s per lane and 32 rows (6)
   float4 res4[kEpiIt];
+  auto load_res = [&](int h) {
 #pragma unroll
-  for (int k = 0; k < kEpiIt; k++) {
-    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx - rr * kF4;
-    const v4i r = __builtin_nontemporal_load(
-        reinterpret_cast<const v4i*>(p.res + (size_t)min(m0 + rr, p.M - 1) * kH + cb2 * 16 + c4 * 4));
-    res4[k] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z), __int_as_float(r.w));
-  }
+    for (int k = 0; k < kEpiIt; k++) {
+      const int idx = lane + 64 * k, rr = kRows * h + idx / kF4, c4 = idx % kF4;
+      const v4i r = __builtin_nontemporal_load(
+          reinterpret_cast<const v4i*>(p.res + (size_t)min(m0 + rr, p.M - 1) * kH + cb2 * 16 + c4 * 4));
+      res4[k] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z), __int_as_float(r.w));
+    }
+  };
+  load_res(0);
   __syncthreads();  // sQ complete
-  v4i acc2[2][kDnCB];
+  constexpr int kRB = kT / 16;  // 16-row blocks
+  v4i acc2[kRB][kDnCB];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < kRB; i++)
 #pragma unroll
     for (int j = 0; j < kDnCB; j++) acc2[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
   for (int kt = 0; kt < kDnSteps; kt++) {  // fully unrolled ring of kRing steps
-    v4i af[2];
+    v4i af[kRB];
 #pragma unroll
-    for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(&sQ[(i * 16 + fr) * kQPitch + kt * 64 + fq * 16]);
+    for (int i = 0; i < kRB; i++) af[i] = *reinterpret_cast<const v4i*>(&sQ[(i * 16 + fr) * kQPitch + kt * 64 + fq * 16]);
 #pragma unroll
     for (int j = 0; j < kDnCB; j++)
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < kRB; i++)
         acc2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], ring[kt % kRing][j], acc2[i][j], 0, 0, 0);
     if (kt + kRing < kDnSteps) load_b2(kt + kRing, ring[kt % kRing]);
   }
 
-  // ---- epilogue of FFN-down through this wave's LDS tile, whole float4s per lane ----
-  int* E = sE[wave];
+  // ---- epilogue of FFN-down through this wave's LDS tile, whole float4s per lane, 32 rows at a time ----
+  if constexpr (kP > 1) __syncthreads();  // every wave is done with sQ, whose space the staging reuses
+  int* E = (kP == 1 ? sE1 : reinterpret_cast<int*>(sQ)) + wave * kEWords;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int h = 0; h < kP; h++) {
+    if (h > 0) {
+      wave_lds_sync();  // the previous half's reads are done
+      load_res(h);      // (its HBM latency is exposed once per 64 rows)
+    }
 #pragma unroll
-    for (int j = 0; j < kDnCB; j++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) E[(i * 16 + fq * 4 + r) * kEPitch + j * 16 + fr] = acc2[i][j][r];
-  wave_lds_sync();
+      for (int j = 0; j < kDnCB; j++)
 #pragma unroll
-  for (int k = 0; k < kEpiIt; k++) {
-    const int idx = lane + 64 * k, rr = idx / kF4, c4 = idx - rr * kF4;
-    const int row = m0 + rr;
-    const bool ok = row < p.M;
-    const int col = cb2 * 16 + c4 * 4;
-    const float s = row_absmax(rr) / 127.0f;  // scale = max_abs / 127.0
-    const int4 a4 = *reinterpret_cast<const int4*>(&E[rr * kEPitch + c4 * 4]);
-    const float4 ws4 = *reinterpret_cast<const float4*>(p.w2_scale + col);
-    float4 b4 = *reinterpret_cast<const float4*>(p.b2 + col);
-    const float4 r4 = res4[k];
-    b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
-    float4 v;
-    v.x = fmaf((float)a4.x, s * ws4.x, b4.x);
-    v.y = fmaf((float)a4.y, s * ws4.y, b4.y);
-    v.z = fmaf((float)a4.z, s * ws4.z, b4.z);
-    v.w = fmaf((float)a4.w, s * ws4.w, b4.w);
-    if (ok)  // streaming store: keeps the weights resident in L2
-      __builtin_nontemporal_store(v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)},
-                                  reinterpret_cast<v4i*>(p.out + (size_t)row * kH + col));
+        for (int r = 0; r < 4; r++) E[(i * 16 + fq * 4 + r) * kEPitch + j * 16 + fr] = acc2[2 * h + i][j][r];
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < kEpiIt; k++) {
+      const int idx = lane + 64 * k, er = idx / kF4, c4 = idx - er * kF4, rr = kRows * h + er;
+      const int row = m0 + rr;
+      const bool ok = row < p.M;
+      const int col = cb2 * 16 + c4 * 4;
+      const float s = row_absmax(rr) / 127.0f;  // scale = max_abs / 127.0
+      const int4 a4 = *reinterpret_cast<const int4*>(&E[er * kEPitch + c4 * 4]);
+      const float4 ws4 = *reinterpret_cast<const float4*>(p.w2_scale + col);
+      float4 b4 = *reinterpret_cast<const float4*>(p.b2 + col);
+      const float4 r4 = res4[k];
+      b4.x = b4.x + r4.x; b4.y = b4.y + r4.y; b4.z = b4.z + r4.z; b4.w = b4.w + r4.w;
+      float4 v;
+      v.x = fmaf((float)a4.x, s * ws4.x, b4.x);
+      v.y = fmaf((float)a4.y, s * ws4.y, b4.y);
+      v.z = fmaf((float)a4.z, s * ws4.z, b4.z);
+      v.w = fmaf((float)a4.w, s * ws4.w, b4.w);
+      if (ok)  // streaming store: keeps the weights resident in L2
+        __builtin_nontemporal_store(v4i{__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)},
+                                    reinterpret_cast<v4i*>(p.out + (size_t)row * kH + col));
+    }
   }
 }
 
+// 64-row workgroups stream W2 once per 64 rows instead of twice, at about 1.87x
+// the time of a 32-row one (measured at C5); with one workgroup per CU, a launch
+// takes about as many such times as it has rounds of workgroups over the CUs, so
+// the 64-row form is chosen when its rounds cost less.
+static int g_ffn_rows = 0;  // 0 by the batch, else 32 or 64 (test hook)
+void set_ffn_rows(int rows) { g_ffn_rows = rows; }
+
 void launch_ffn(const FfnArgs& p, hipStream_t st) {
   if (p.M <= 0) return;
-  hipLaunchKernelGGL(ffn_fused_kernel, dim3((p.M + kRows - 1) / kRows), dim3(512), 0, st, p);
+  const int cus = device_cu_count();
+  const long t32 = (p.M + kRows - 1) / kRows, t64 = (p.M + 2 * kRows - 1) / (2 * kRows);
+  const long r32 = (t32 + cus - 1) / cus, r64 = (t64 + cus - 1) / cus;
+  if (g_ffn_rows == 64 || (g_ffn_rows == 0 && 100 * r32 > 187 * r64))
+    hipLaunchKernelGGL(ffn_fused_kernel<2>, dim3((unsigned)t64), dim3(512), 0, st, p);
+  else
+    hipLaunchKernelGGL(ffn_fused_kernel<1>, dim3((unsigned)t32), dim3(512), 0, st, p);
 }
 
 }  // namespace aek

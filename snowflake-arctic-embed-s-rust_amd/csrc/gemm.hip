@@ -1040,7 +1040,7 @@ __global__ __launch_bounds__(512) void gemm_small_kernel(GemmArgs p, LnArgs ln, 
 constexpr int kSmallM = 1024;
 
 // compute units of the current device (cached per device; 256 on MI355X)
-static int device_cu_count() {
+int device_cu_count() {
   static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

@@ -57,6 +57,10 @@ struct FfnArgs {
   float* out;              // [M,384]
 };
 void launch_ffn(const FfnArgs& p, hipStream_t st);
+// token rows per FFN workgroup, process-wide (a test hook): 0 by the batch (default), 32 or 64
+void set_ffn_rows(int rows);
+// compute units of the current device (cached per device)
+int device_cu_count();
 
 constexpr int kLnSrcF32 = 0;
 constexpr int kLnSrcEmb = 1;

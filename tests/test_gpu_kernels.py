@@ -217,13 +217,23 @@ def test_gemm_gelu_epilogue_bit_exact(torch_gpu, m):
     assert np.array_equal(rowmax / f32(127), sc)
 
 
-@pytest.mark.parametrize("m,in_place", [(1, False), (31, False), (33, True), (100, False), (4133, True)])
-def test_ffn_fused_bit_exact(torch_gpu, m, in_place):
+@pytest.fixture(params=[32, 64], ids=["rows32", "rows64"])
+def ffn_rows(request, torch_gpu):
+    """Every fused-FFN test runs with 32-row and with 64-row workgroups."""
+    ae.set_ffn_rows(request.param)
+    yield request.param
+    ae.set_ffn_rows(0)
+
+
+@pytest.mark.parametrize("m,in_place", [(1, False), (31, False), (33, True), (64, False), (100, False),
+                                        (4133, True)])
+def test_ffn_fused_bit_exact(torch_gpu, ffn_rows, m, in_place):
     """The one-kernel FFN block (FFN-up + GELU * inv_smooth + row absmax int8
     quantization + FFN-down + bias + residual) against the oracle's three steps
-    (src/model.rs:725-755): bit-exact, including partial last workgroups and
-    out == res."""
+    (src/model.rs:725-755): bit-exact, including partial last workgroups (and
+    partial second passes of 64-row ones) and out == res."""
     torch = torch_gpu
+    print("ffn rows", ffn_rows, "m", m, flush=True)
     w1, ws1, b1, s1 = linear_inputs(1536, 384, 7)
     w2, ws2, b2, s2 = linear_inputs(384, 1536, 8)
     rng = np.random.default_rng(m + 11)
@@ -242,27 +252,29 @@ def test_ffn_fused_bit_exact(torch_gpu, m, in_place):
     assert np.array_equal(bits(out_d.cpu().numpy()), bits(ref))
 
 
-def test_ffn_fused_extreme_rows(torch_gpu):
+def test_ffn_fused_extreme_rows(torch_gpu, ffn_rows):
     """The fused FFN on rows that drive the GELU to its extremes: saturated int8
     rows (|pre-activation| up to ~1e3, GELU -> 0 or x), tiny scales (GELU near
     0, the 1e-8 absmax floor), a single nonzero column, and rows of equal values
-    (quantization ties)."""
+    (quantization ties); the same rows again from row 32 (the second pass of a
+    64-row workgroup)."""
     torch = torch_gpu
     w1, ws1, b1, s1 = linear_inputs(1536, 384, 21)
     w2, ws2, b2, s2 = linear_inputs(384, 1536, 22)
-    m = 40
+    m = 72
     rng = np.random.default_rng(23)
     a = rng.integers(-127, 128, (m, 384), dtype=np.int8)
-    a[1:5] = 127
-    a[5:9] = -127
-    a[9] = 0
-    a[10] = 0
-    a[10, 17] = 127
-    a[11:14] = 64
     sa = rng.uniform(0.01, 0.1, m).astype(f32)
-    sa[1:3] = 40.0                      # huge pre-activations
-    sa[14:18] = np.float32(1e-30)       # GELU inputs ~ bias only
-    sa[18] = 0.0
+    for o in (0, 32):
+        a[o + 1:o + 5] = 127
+        a[o + 5:o + 9] = -127
+        a[o + 9] = 0
+        a[o + 10] = 0
+        a[o + 10, 17] = 127
+        a[o + 11:o + 14] = 64
+        sa[o + 1:o + 3] = 40.0                  # huge pre-activations
+        sa[o + 14:o + 18] = np.float32(1e-30)   # GELU inputs ~ bias only
+        sa[o + 18] = 0.0
     res = rng.normal(0, 1, (m, 384)).astype(f32)
     up, down = ae.Linear(w1, ws1, b1, s1), ae.Linear(w2, ws2, b2, s2)
     a_d, sa_d, res_d = dev(torch, a), dev(torch, sa), dev(torch, res)
