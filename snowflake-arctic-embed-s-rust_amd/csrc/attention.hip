@@ -14,7 +14,7 @@ namespace aek {
 // (src/model.rs:663-694 with compute_scores_head32 / softmax_inplace /
 // weighted_sum_head32 scalar branches, src/simd_math.rs:1461-1821):
 //   s_t  = (sum_{i=0..31, in order} q_i*k_t,i) * (1/sqrt(32))
-//   e_t  = expf(s_t - max_t s_t)            (glibc expf, restated above)
+//   e_t  = expf(s_t - max_t s_t)            (glibc expf: expf_libm, device_common.hpp)
 //   sum  = sum_{t in order} e_t ; inv = 1/sum ; p_t = e_t * inv
 //   ctx_d = sum_{t in order} p_t * v_t,d
 // every sum left to right with separately rounded products.
