@@ -1059,6 +1059,22 @@ void launch_attention_short(const AttnArgs& p, hipStream_t st) {
 // LDS tile and many fit on a CU.  Keys past p.max_len (<= 512) are not attended
 // (the embedding kernel reports such sequences through the workspace's error
 // word).
+// float4 i of the [CLS] row (token s0) of hidden: as stored, or (hidden_stats)
+// the LayerNorm output of that row, recomputed as the LayerNorm forms it
+__device__ __forceinline__ float4 cls_hidden_row(const ClsArgs& p, int s0, int i) {
+  float4 v = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[i];
+  if (p.hidden_stats) {
+    const float2 st = p.hidden_stats[s0];
+    const float4 g = reinterpret_cast<const float4*>(p.ln_gamma)[i];
+    const float4 bt = reinterpret_cast<const float4*>(p.ln_beta)[i];
+    v.x = (v.x - st.x) * st.y * g.x + bt.x;
+    v.y = (v.y - st.x) * st.y * g.y + bt.y;
+    v.z = (v.z - st.x) * st.y * g.z + bt.z;
+    v.w = (v.w - st.x) * st.y * g.w + bt.w;
+  }
+  return v;
+}
+
 __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
   __shared__ __attribute__((aligned(16))) float S[512];
   __shared__ __attribute__((aligned(16))) float sQ[32];
@@ -1082,7 +1098,7 @@ __global__ __launch_bounds__(256) void cls_attention_kernel(ClsArgs p) {
     }
   }
   if (h == 0 && tid < 96)  // gather the [CLS] row of hidden (the tail's residual)
-    reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[tid] = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[tid];
+    reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[tid] = cls_hidden_row(p, s0, tid);
   float4 kr[2][8];
 #pragma unroll
   for (int u = 0; u < 2; u++) {
@@ -1378,8 +1394,7 @@ __global__ __launch_bounds__(256, 6) void cls_attention_short_kernel(ClsArgs p) 
   for (int off = 1; off < 64; off <<= 1) a = nanless_max(a, __shfl_xor(a, off, 64));
   if (lane == 0) atomicMax(&p.rowmax_ctx_c[b], __float_as_uint(a));
   if (h == 0)  // gather the [CLS] row of hidden (the tail's residual), last: no registers held meanwhile
-    for (int i = lane; i < 96; i += 64)
-      reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[i] = reinterpret_cast<const float4*>(p.hidden + (size_t)s0 * H)[i];
+    for (int i = lane; i < 96; i += 64) reinterpret_cast<float4*>(p.hidden_c + (size_t)b * H)[i] = cls_hidden_row(p, s0, i);
 }
 
 void launch_cls(const ClsArgs& p, hipStream_t st) {

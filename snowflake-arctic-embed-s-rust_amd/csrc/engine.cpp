@@ -151,6 +151,7 @@ struct ae_workspace {
   int8_t* act_q = nullptr;
   float* act_scale = nullptr;
   uint32_t *rowmax_ctx = nullptr, *rowmax_g = nullptr;
+  float2* ln2_stats = nullptr;  // [T]: LN2's (mean, rstd) per row, when the next layer recomputes its output
   float *hidden_c = nullptr, *tmp_c = nullptr, *ctx_c = nullptr, *g_c = nullptr, *out_c = nullptr;
   int8_t* act_q_c = nullptr;
   float* act_scale_c = nullptr;
@@ -418,6 +419,13 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   const bool small = gemm_small_path(T);
   const float* ln2_w = nullptr;  // small: the previous layer's LN2, applied by the next QKV prologue
   const float* ln2_b = nullptr;
+  // With the fused FFN (many rows), LN2 writes its (mean, rstd) per row instead
+  // of its f32 output: the next attention-output kernel, its only reader,
+  // recomputes that output from LN2's input rows (tmp) as LN2 forms it, and the
+  // [CLS] gather of layer 11 does so for its rows.  This saves LN2's f32 store
+  // (T x 1536 bytes per layer).  The last layer of a truncated pass
+  // (stop_layers) still stores it: it is the state returned.
+  const bool ln2_stats = !small && T >= kFfnFusedMinRows;
   for (int l = 0; l < ae::kLayers - 1; l++) {  // src/model.rs:593-768
     if (stop_layers >= 0 && l >= stop_layers) break;
     const DevLayer& D = E->layers[l];
@@ -470,14 +478,25 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
       ln2_b = D.ln2_b;
       continue;
     }
-    gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1,
-                 gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden, ws->tmp,
-                           nullptr, nullptr),
-                 kAF32QSmooth,
-                 ln_args(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale,
-                         ws->rowmax_g, T));
-    const LnArgs ln2 = ln_args(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q,
-                               ws->act_scale, ws->rowmax_ctx, T);
+    {
+      GemmArgs g = gemm_args(D.attn_out, T, ws->ctx, nullptr, ws->rowmax_ctx, D.attn_out.inv_smooth, ws->hidden,
+                             ws->tmp, nullptr, nullptr);
+      if (ln2_stats && l > 0) {  // the residual: the previous layer's LN2 of tmp, recomputed
+        g.res = ws->tmp;
+        g.res_stats = ws->ln2_stats;
+        g.res_gamma = E->layers[l - 1].ln2_w;
+        g.res_beta = E->layers[l - 1].ln2_b;
+      }
+      gemm_then_ln(AE_KERNEL_GEMM_ATTN_OUT, AE_KERNEL_LN1, g, kAF32QSmooth,
+                   ln_args(ws->tmp, ws->hidden, D.ln1_w, D.ln1_b, D.ffn_inter.inv_smooth, ws->act_q, ws->act_scale,
+                           ws->rowmax_g, T));
+    }
+    LnArgs ln2 = ln_args(ws->tmp, ws->hidden, D.ln2_w, D.ln2_b, E->layers[l + 1].qkv_smooth, ws->act_q,
+                         ws->act_scale, ws->rowmax_ctx, T);
+    if (ln2_stats) {
+      ln2.stats = ws->ln2_stats;
+      if (!(stop_layers >= 0 && l + 1 == stop_layers)) ln2.dst = nullptr;
+    }
     if (T >= kFfnFusedMinRows) {  // FFN-up, GELU, quantize and FFN-down in one kernel
       {
         KernelTimer kt(ws, st, AE_KERNEL_GEMM_FFN_UP);
@@ -535,6 +554,12 @@ int run_forward(ae_workspace* ws, const uint16_t* ids, const int* cu, int B, int
   c.smooth = D.attn_out.inv_smooth;
   c.rowmax_ctx_c = ws->rowmax_ctx_c;  // reset by the embedding kernel
   c.max_len = std::min(max_len, ae::kMaxPos);
+  if (ln2_stats) {  // layer 10's LN2 output for the [CLS] rows, recomputed from tmp
+    c.hidden = ws->tmp;
+    c.hidden_stats = ws->ln2_stats;
+    c.ln_gamma = E->layers[ae::kLayers - 2].ln2_w;
+    c.ln_beta = E->layers[ae::kLayers - 2].ln2_b;
+  }
   launch_cls(c, st);
   if (small_tail) {  // attention output + LN1 + FFN-up in one kernel (rowmax_g_c reset by the embedding kernel)
     const PreArgs pre{ws->ctx_c, ws->rowmax_ctx_c, D.attn_out.inv_smooth, D.attn_out.w, D.attn_out.w_scale,
@@ -778,6 +803,7 @@ int ae_workspace_create(const ae_engine* e, size_t max_tokens, size_t max_seqs, 
       (rc = A(&ws->hidden, T * 384)) || (rc = A(&ws->tmp, T * 384)) || (rc = A(&ws->qkv, T * 1152)) ||
       (rc = A(&ws->ctx, T * 384)) || (rc = A(&ws->g, T * 1536)) || (rc = A(&ws->act_q, T * 384)) ||
       (rc = A(&ws->act_scale, T)) || (rc = A(&ws->rowmax_ctx, T)) || (rc = A(&ws->rowmax_g, T)) ||
+      (rc = A(&ws->ln2_stats, T)) ||
       (rc = A(&ws->hidden_c, B * 384)) || (rc = A(&ws->tmp_c, B * 384)) ||
       (rc = A(&ws->ctx_c, B * 384)) || (rc = A(&ws->g_c, B * 1536)) || (rc = A(&ws->out_c, B * 384)) ||
       (rc = A(&ws->act_q_c, B * 384)) || (rc = A(&ws->act_scale_c, B)) || (rc = A(&ws->rowmax_ctx_c, B)) ||

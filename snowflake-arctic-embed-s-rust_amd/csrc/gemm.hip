@@ -407,6 +407,12 @@ __global__ __launch_bounds__(256, 3) void gemm_ln_rows_kernel(GemmArgs p, LnArgs
   int8_t* sA = reinterpret_cast<int8_t*>(sT);
   __shared__ __attribute__((aligned(16))) float sWs[384], sB[384];
   __shared__ float s_mean[kLrRows], s_rstd[kLrRows];
+  // res_stats: res_gamma / res_beta in the row tile's space past the A tile,
+  // free until the accumulators are written (after the residual is formed)
+  constexpr int kRgOff = 4096;  // floats (the A tile takes 32 x 400 bytes)
+  static_assert(kLrRows * kAsPitch <= 4 * kRgOff && kRgOff + 768 <= kLrRows * kLrPitch, "residual LN parameters fit");
+  float* sRg = sT + kRgOff;
+  float* sRb = sRg + 384;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fq = lane >> 4;
   const int m0 = blockIdx.x * kLrRows;
@@ -435,6 +441,10 @@ __global__ __launch_bounds__(256, 3) void gemm_ln_rows_kernel(GemmArgs p, LnArgs
   for (int u = 0; u < kRing; u++) wload(u, ring[u]);
   if (tid < 96) reinterpret_cast<float4*>(sWs)[tid] = reinterpret_cast<const float4*>(p.w_scale)[tid];
   else if (tid < 192) reinterpret_cast<float4*>(sB)[tid - 96] = reinterpret_cast<const float4*>(p.bias)[tid - 96];
+  if (p.res_stats) {
+    if (tid < 96) reinterpret_cast<float4*>(sRg)[tid] = reinterpret_cast<const float4*>(p.res_gamma)[tid];
+    else if (tid < 192) reinterpret_cast<float4*>(sRb)[tid - 96] = reinterpret_cast<const float4*>(p.res_beta)[tid - 96];
+  }
 
   {  // A quantized as kAF32QSmooth: q = round((x * inv_smooth[j]) * (127 / max_abs))
     const float inv = 127.0f / amax_a;  // inv_scale = 127.0 / max_abs
@@ -472,6 +482,19 @@ __global__ __launch_bounds__(256, 3) void gemm_ln_rows_kernel(GemmArgs p, LnArgs
   for (int i = 0; i < 12; i++) {
     const v4i r = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(rr + (sub + 8 * i) * 4));
     res[i] = make_float4(__int_as_float(r.x), __int_as_float(r.y), __int_as_float(r.z), __int_as_float(r.w));
+  }
+  if (p.res_stats) {  // the residual is the LayerNorm of these rows, recomputed as that LayerNorm forms it
+    const float2 st = p.res_stats[rrow];
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+      const int c = (sub + 8 * i) * 4;
+      const float4 g = *reinterpret_cast<const float4*>(&sRg[c]);
+      const float4 bt = *reinterpret_cast<const float4*>(&sRb[c]);
+      res[i].x = (res[i].x - st.x) * st.y * g.x + bt.x;
+      res[i].y = (res[i].y - st.x) * st.y * g.y + bt.y;
+      res[i].z = (res[i].z - st.x) * st.y * g.z + bt.z;
+      res[i].w = (res[i].w - st.x) * st.y * g.w + bt.w;
+    }
   }
   __syncthreads();  // every wave's K loop is done with the A tile
   // accumulators into the row tile (lane: rows 16 i + 4 fq + r of column 96 w + 16 j + fr)

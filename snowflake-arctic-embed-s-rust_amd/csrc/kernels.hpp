@@ -32,6 +32,13 @@ struct GemmArgs {
   const float* g_smooth;      // kEpiGelu: next layer inv_smooth [N]
   uint32_t* g_rowmax;         // kEpiGelu: [M], pre-set to bits(1e-8f)
   int col_fast;               // set by launch_gemm: workgroup order (column tile fastest)
+  // gemm_ln_rows_kernel only (launch_gemm_ln's many-rows path; the caller sets
+  // them only there): res holds a LayerNorm's input rows, and the residual is
+  // that LayerNorm's output, recomputed as ((res - mean) * rstd) * res_gamma +
+  // res_beta from its (mean, rstd) per row
+  const float2* res_stats = nullptr;
+  const float* res_gamma = nullptr;
+  const float* res_beta = nullptr;
   int stream_cols = 0;        // output columns [0, stream_cols) are stored nontemporally (read once later)
 };
 // N % 384 == 0, K % 64 == 0
@@ -80,7 +87,8 @@ struct LnArgs {
   const float* gamma;
   const float* beta;
   const float* smooth;
-  float* dst;       // LayerNorm output (f32 residual stream), may alias src
+  float* dst;       // LayerNorm output (f32 residual stream), may alias src; may be null (stats instead)
+  float2* stats;    // optional: (mean, rstd) per row, from which a consumer recomputes the output exactly
   int8_t* q;        // [T,384]
   float* scale;     // [T]
   uint32_t* rowmax_init;   // optional: set to bits(1e-8f) for each row
@@ -205,6 +213,11 @@ struct ClsArgs {
   const float* smooth;     // attn_out inv_smooth
   uint32_t* rowmax_ctx_c;  // [B], pre-set to bits(1e-8f)
   int max_len = 512;       // keys attended per sequence (<= 512): sizes the V tile in LDS
+  // optional: hidden holds a LayerNorm's input rows and hidden_c gets that
+  // LayerNorm's output, ((x - mean) * rstd) * ln_gamma + ln_beta per row
+  const float2* hidden_stats = nullptr;
+  const float* ln_gamma = nullptr;
+  const float* ln_beta = nullptr;
 };
 // the layer-11 [CLS] attention: per (sequence, head) the [CLS] row's q (the q_only
 // GEMM for that row and head), its attention over the segment's K/V rows, ctx_c

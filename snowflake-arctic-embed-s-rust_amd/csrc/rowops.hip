@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
     y.y = (xv[i].y - mean) * rstd * g.y + b.y;
     y.z = (xv[i].z - mean) * rstd * g.z + b.z;
     y.w = (xv[i].w - mean) * rstd * g.w + b.w;
-    if (valid) *reinterpret_cast<float4*>(p.dst + (size_t)row * H + c) = y;
+    if (valid && p.dst) *reinterpret_cast<float4*>(p.dst + (size_t)row * H + c) = y;
     ys[i] = make_float4(y.x * s.x, y.y * s.y, y.z * s.z, y.w * s.w);
     amax = nanless_max(amax, fabsf(ys[i].x));
     amax = nanless_max(amax, fabsf(ys[i].y));
@@ -147,6 +147,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
     }
     if (sub == 0) {
       p.scale[row] = max_abs / 127.0f;
+      if (p.stats) p.stats[row] = make_float2(mean, rstd);
       if (p.rowmax_init) p.rowmax_init[row] = __float_as_uint(1e-8f);
       if (p.rowmax_init2) p.rowmax_init2[row] = __float_as_uint(1e-8f);
       if (SRC == kLnSrcEmb && row < p.n_c) {
