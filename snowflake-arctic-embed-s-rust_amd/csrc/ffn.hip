@@ -121,7 +121,7 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
     // their pointers keep the compiler from hoisting the 36 loads out of the
     // pass loop (and holding 36 more registers through the GELUs)
     const float *w1s = p.w1_scale, *b1 = p.b1, *gsm = p.g_smooth;
-    asm volatile("" : "+s"(w1s), "+s"(b1), "+s"(gsm));
+    if constexpr (kP > 1) asm volatile("" : "+s"(w1s), "+s"(b1), "+s"(gsm));
     auto mma_col = [&](int j, const v4i* bf) {
 #pragma unroll
       for (int i = 0; i < 2; i++) acc[i][j] = v4i{0, 0, 0, 0};
