@@ -71,7 +71,9 @@ def kernel_work(kind, T, B, lens):
 def roofline_step_ms(T, B, lens, ffn_fused=False, attn_ln_fused=False):
     """Ideal time of one forward pass: the sum over launches of max(ops / peak, bytes / HBM) with
     algorithmic ops and bytes (weights read once per launch), per kernel kind (ms per step).
-    ffn_fused: the FFN block is one kernel (int8 A, f32 residual and output, no intermediate).
+    ffn_fused: the FFN block is one kernel (int8 A, f32 residual and output, no intermediate), and
+    LN2 then stores (mean, rstd) per row instead of its f32 output (the next attention-output
+    kernel recomputes it from LN2's input rows).
     attn_ln_fused: the attention output GEMM and LN1 are one kernel (f32 ctx and residual in, the
     LayerNorm's f32 row, int8 row and scale out; no intermediate)."""
     sum_l2 = float(sum(int(L) * int(L) for L in lens))
@@ -90,7 +92,7 @@ def roofline_step_ms(T, B, lens, ffn_fused=False, attn_ln_fused=False):
         "ln1": 11 * T * (384 * 4 * 2 + 384 + 4) / hbm,
         "gemm_ffn_up": 11 * gemm(T, 1536, 384, 1, False),
         "gemm_ffn_down": 11 * gemm(T, 384, 1536, 4, True),
-        "ln2": 11 * T * (384 * 4 * 2 + 384 + 4) / hbm,
+        "ln2": 11 * T * (384 * 4 + (8 if ffn_fused else 384 * 4) + 384 + 4) / hbm,
         "ffn_fused": 11 * max(4.0 * T * 1536 * 384 / (PEAK_INT8_TOPS * 1e12),
                               (T * (384 + 4 + 2 * 384 * 4) + 2 * 1536 * 384 + 1536 * 12 + 384 * 8) / hbm),
         # layer 11: K/V for all tokens, the [CLS] query's attention over them, then the B-row tail
