@@ -29,9 +29,10 @@ namespace aek {
 constexpr int kAttnQ = 32;     // queries per workgroup
 // In batches of mostly shorter rows (launch_attention), the tiles of rows of at
 // most kAttnLongL keys and those of longer rows go to two launches: score tiles
-// of at most 32 x (kAttnLongL + 4) floats (49.7 KB, three workgroups per CU) in
-// the first, up to 32 x 516 floats (66 KB, two per CU) in the second.
-constexpr int kAttnLongL = 384;
+// of at most 32 x (kAttnLongL + 4) floats (51.7 KB, three workgroups per CU) in
+// the first, up to 32 x 516 floats (66 KB, two per CU) in the second.  (At 416
+// keys, 53.8 KB, C3 ran 6 % slower, as with two workgroups per CU.)
+constexpr int kAttnLongL = 400;
 
 // Work plan, built on the device from cu_seqlens: one 16-byte record per tile
 // of kAttnQ queries, {s0, L, q0, nq} = the segment's first token, its length,
