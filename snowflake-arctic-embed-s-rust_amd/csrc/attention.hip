@@ -947,8 +947,10 @@ void init_attention_kernels() {
 // and latency-bound, run faster with the narrow one's 6.  The choice is by the
 // batch's mean length (both variants give the same bits).
 constexpr int kWideMinMeanLen = 48;
-// mean length up to which the rows over kAttnLongL keys get a launch of their own
-constexpr int kSplitMaxMean = 320;
+// mean length up to which the rows over kAttnLongL keys get a launch of their
+// own (above it, nearly every row is long and the short rows' launch would be
+// empty: its workgroups still cost C4 0.4 %)
+constexpr int kSplitMaxMean = 448;
 
 void launch_attention_plan(const AttnArgs& p, hipStream_t st, int split, int max_tiles) {
   hipLaunchKernelGGL(attention_plan_kernel, dim3(1), dim3(256), 0, st, p.cu, p.B, p.s_pitch - 4, max_tiles, split,

@@ -355,12 +355,13 @@ def test_gelu_bit_exact_over_float_sample(torch_gpu):
 # form (at most 16 tiles of 32 queries, longest > 64), register-resident rows
 # (longest <= 32, <= 64), else the tiled kernel with the wide (mean > 48) or the
 # narrow operand layout; these length sets reach each.  The tiled kernel runs the
-# rows of more than 384 keys in a launch of their own when the batch's mean
-# length is at most 320 ("tiled_long": both sides of 384, with short rows), else
-# every row in one launch ("tiled_long32")
+# rows of more than 400 keys in a launch of their own when the batch's mean
+# length is at most 448 ("tiled_long": both sides of 400, with short rows;
+# "tiled_long_mean410"), else every row in one launch ("tiled_long32")
 ATTN_LENS = {"tiled_wide": [1, 2, 17, 31, 32, 33, 64, 65, 130, 512, 3],
-             "tiled_long": [384, 385, 17, 408, 409, 431, 1, 449, 480, 500, 511, 512, 24, 25, 200],
-             "tiled_long32": [512, 500, 450, 400, 385, 512, 480, 449, 33, 384],
+             "tiled_long": [384, 385, 17, 400, 401, 408, 409, 431, 1, 449, 480, 500, 511, 512, 24, 25, 200],
+             "tiled_long_mean410": [512, 500, 450, 400, 385, 512, 480, 449, 33, 384],
+             "tiled_long32": [512, 500, 480, 512, 449, 512, 470, 300, 505, 512, 490, 401],
              "tiled_narrow": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 100],
              "rows64": [1, 2, 17, 31, 32, 33, 3, 9, 16, 15, 40, 8, 64],
              "rows32": [1, 2, 17, 31, 32, 3, 9, 16, 15, 8],
