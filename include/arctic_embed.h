@@ -304,8 +304,10 @@ int ae_debug_mfma_products(const float* a_dev, const float* b_dev, float* out_de
  * gives the same bits.  AE_ERR_INVALID_ARG for another value. */
 int ae_debug_set_attention_form(int form);
 /* Token rows per workgroup of the fused FFN kernel, process-wide (a test hook,
- * no reference counterpart): 0 by the batch's size (the default), 32 or 64.
- * Both heights give the same bits.  AE_ERR_INVALID_ARG for another value. */
+ * no reference counterpart): 0 by the batch's size (the default), 32 or 64, or
+ * -m (m a multiple of 64): the first m rows in 64-row workgroups and the rest
+ * in a second launch of 32-row ones.  Every plan gives the same bits.
+ * AE_ERR_INVALID_ARG for another value. */
 int ae_debug_set_ffn_rows(int rows);
 
 #ifdef __cplusplus

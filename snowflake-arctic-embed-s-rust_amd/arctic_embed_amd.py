@@ -483,5 +483,6 @@ def set_attention_form(form):
 
 def set_ffn_rows(rows):
     """Token rows per workgroup of the fused FFN kernel from now on: 0 by the
-    batch (default), 32 or 64 (a test hook)."""
+    batch (default), 32 or 64, or -m: the first m rows (a multiple of 64) in 64-row
+    workgroups, the rest in 32-row ones (a test hook)."""
     _check(_lib.ae_debug_set_ffn_rows(int(rows)))

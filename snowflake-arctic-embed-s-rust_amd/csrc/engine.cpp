@@ -1354,7 +1354,8 @@ int ae_debug_set_attention_form(int form) {
 
 // test hook: the FFN kernel's workgroup height
 int ae_debug_set_ffn_rows(int rows) {
-  if (rows != 0 && rows != 32 && rows != 64) return fail(AE_ERR_INVALID_ARG, "FFN rows must be 0, 32 or 64");
+  if (rows != 0 && rows != 32 && rows != 64 && !(rows < 0 && rows % 64 == 0))
+    return fail(AE_ERR_INVALID_ARG, "FFN rows must be 0, 32, 64 or a negative multiple of 64");
   aek::set_ffn_rows(rows);
   return AE_OK;
 }

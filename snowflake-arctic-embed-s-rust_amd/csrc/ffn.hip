@@ -304,21 +304,48 @@ __global__ __launch_bounds__(512, 2) void ffn_fused_kernel(FfnArgs p) {
 }
 
 // 64-row workgroups stream W2 once per 64 rows instead of twice, at about 1.87x
-// the time of a 32-row one (measured at C5); with one workgroup per CU, a launch
-// takes about as many such times as it has rounds of workgroups over the CUs, so
-// the 64-row form is chosen when its rounds cost less.
-static int g_ffn_rows = 0;  // 0 by the batch, else 32 or 64 (test hook)
+// the time of a 32-row one (measured at C5).  With one workgroup per CU, a
+// launch takes about as many workgroup times as it has rounds of workgroups over
+// the CUs, so launch_ffn picks, in 32-row workgroup times, the cheapest of: all
+// rows in 32-row workgroups, all in 64-row ones, or k full rounds of 64-row
+// workgroups followed by a second launch of 32-row ones for the remaining rows
+// (its last, partial round then holds the short workgroups).
+static int g_ffn_rows = 0;  // 0 by the batch, 32, 64, or -m: the mixed plan with m rows first (test hook)
 void set_ffn_rows(int rows) { g_ffn_rows = rows; }
 
 void launch_ffn(const FfnArgs& p, hipStream_t st) {
   if (p.M <= 0) return;
-  const int cus = device_cu_count();
-  const long t32 = (p.M + kRows - 1) / kRows, t64 = (p.M + 2 * kRows - 1) / (2 * kRows);
-  const long r32 = (t32 + cus - 1) / cus, r64 = (t64 + cus - 1) / cus;
-  if (g_ffn_rows == 64 || (g_ffn_rows == 0 && 100 * r32 > 187 * r64))
-    hipLaunchKernelGGL(ffn_fused_kernel<2>, dim3((unsigned)t64), dim3(512), 0, st, p);
-  else
-    hipLaunchKernelGGL(ffn_fused_kernel<1>, dim3((unsigned)t32), dim3(512), 0, st, p);
+  const long cus = device_cu_count();
+  auto rounds = [&](long rows, long tile) { return ((rows + tile - 1) / tile + cus - 1) / cus; };
+  constexpr long kT64 = 187;  // a 64-row workgroup's time, in hundredths of a 32-row one
+  long best = 100 * rounds(p.M, 32), best_k = -1;  // -1: all 32-row, 0: all 64-row, k: mixed
+  if (100 * rounds(p.M, 32) > kT64 * rounds(p.M, 64)) best = kT64 * rounds(p.M, 64), best_k = 0;
+  for (long k = 1; 64 * cus * k < p.M; k++) {
+    const long t = kT64 * k + 100 * rounds(p.M - 64 * cus * k, 32) + 10;  // + a second launch
+    if (t < best) best = t, best_k = k;
+  }
+  if (g_ffn_rows == 32) best_k = -1;
+  if (g_ffn_rows == 64) best_k = 0;
+  int m64 = (int)(64 * cus * (best_k > 0 ? best_k : 0));
+  if (g_ffn_rows < 0) {  // forced mixed plan (m64 rows in 64-row workgroups, when there are more)
+    m64 = -g_ffn_rows;
+    best_k = m64 < p.M ? 1 : 0;
+  }
+  if (best_k < 0) {
+    hipLaunchKernelGGL(ffn_fused_kernel<1>, dim3((unsigned)((p.M + 31) / 32)), dim3(512), 0, st, p);
+  } else if (best_k == 0) {
+    hipLaunchKernelGGL(ffn_fused_kernel<2>, dim3((unsigned)((p.M + 63) / 64)), dim3(512), 0, st, p);
+  } else {
+    FfnArgs a = p, b = p;
+    a.M = m64;
+    b.M = p.M - m64;
+    b.A = p.A + (size_t)m64 * kH;
+    b.a_scale = p.a_scale + m64;
+    b.res = p.res + (size_t)m64 * kH;
+    b.out = p.out + (size_t)m64 * kH;
+    hipLaunchKernelGGL(ffn_fused_kernel<2>, dim3((unsigned)(m64 / 64)), dim3(512), 0, st, a);
+    hipLaunchKernelGGL(ffn_fused_kernel<1>, dim3((unsigned)((b.M + 31) / 32)), dim3(512), 0, st, b);
+  }
 }
 
 }  // namespace aek

@@ -217,9 +217,11 @@ def test_gemm_gelu_epilogue_bit_exact(torch_gpu, m):
     assert np.array_equal(rowmax / f32(127), sc)
 
 
-@pytest.fixture(params=[32, 64], ids=["rows32", "rows64"])
+@pytest.fixture(params=[32, 64, -64], ids=["rows32", "rows64", "mixed64"])
 def ffn_rows(request, torch_gpu):
-    """Every fused-FFN test runs with 32-row and with 64-row workgroups."""
+    """Every fused-FFN test runs with 32-row and with 64-row workgroups, and with
+    the first 64 rows in a 64-row workgroup and the rest in a second launch of
+    32-row ones."""
     ae.set_ffn_rows(request.param)
     yield request.param
     ae.set_ffn_rows(0)
