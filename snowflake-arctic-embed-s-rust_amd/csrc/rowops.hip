@@ -12,21 +12,22 @@ namespace aek {
 // LayerNorm + SmoothQuant + dynamic int8 quantization over 384-wide rows
 // (layernorm_smooth_quantize_row_scalar, reference src/simd_math.rs:208-247).
 //
-// WG = 256 threads, 32 rows.  Phase A stages x into LDS; phase B gives each
+// WG = 128 threads, 16 rows (8 lanes per row).  Phase A stages x into LDS; phase B gives each
 // row to one lane, which forms the mean and variance with the reference's
 // sequential left-to-right sums (the squared deviations are formed by all
 // threads); phase C normalizes, takes the order-free row absmax and quantizes
 // with 8 lanes per row.  Source modes: f32 rows, or the
 // embedding gather ((w*ws + p*ps) + type0, src/simd_math.rs:1877-1880).
 // ---------------------------------------------------------------------------
-constexpr int kLnRows = 32;
+constexpr int kLnRows = 16;
+constexpr int kLnThreads = 8 * kLnRows;  // 8 lanes per row
 constexpr int kLnPitch = 388;
 
 // bit 0 of *err when cu[0..B] is not a prefix sum of T with every segment
-// 1..max_len tokens long; run by the 256 threads of one workgroup
+// 1..max_len tokens long; run by the threads of one workgroup
 __device__ __forceinline__ void check_segments(const int* cu, int B, int T, int max_len, int* err) {
   bool bad = threadIdx.x == 0 && (cu[0] != 0 || cu[B] != T);
-  for (int b = threadIdx.x; b < B; b += 256) {
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
     const int len = cu[b + 1] - cu[b];
     bad = bad || len < 1 || len > max_len;
   }
@@ -36,7 +37,7 @@ __device__ __forceinline__ void check_segments(const int* cu, int B, int T, int 
 // LAT (few rows: latency, not bandwidth, bounds the launch): gamma, beta and
 // inv_smooth are loaded into registers at the start instead of after the sums.
 template <int SRC, bool LAT>
-__global__ __launch_bounds__(256) void ln_quant_kernel(LnArgs p) {
+__global__ __launch_bounds__(kLnThreads) void ln_quant_kernel(LnArgs p) {
   __shared__ __attribute__((aligned(16))) float tile[kLnRows * kLnPitch];
   __shared__ float s_mean[kLnRows], s_rstd[kLnRows];
   float4 pg[LAT ? 12 : 1], pb[LAT ? 12 : 1], ps[LAT ? 12 : 1];
@@ -173,11 +174,11 @@ void launch_ln_quant(const LnArgs& p, int src_mode, hipStream_t st) {
   const int n = (p.T + kLnRows - 1) / kLnRows;
   const bool lat = n <= kLnLatencyGrid;
   if (src_mode == kLnSrcEmb) {
-    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, true>), dim3(n), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, false>), dim3(n), dim3(256), 0, st, p);
+    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, true>), dim3(n), dim3(kLnThreads), 0, st, p);
+    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcEmb, false>), dim3(n), dim3(kLnThreads), 0, st, p);
   } else {
-    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, true>), dim3(n), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, false>), dim3(n), dim3(256), 0, st, p);
+    if (lat) hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, true>), dim3(n), dim3(kLnThreads), 0, st, p);
+    else hipLaunchKernelGGL((ln_quant_kernel<kLnSrcF32, false>), dim3(n), dim3(kLnThreads), 0, st, p);
   }
 }
 
