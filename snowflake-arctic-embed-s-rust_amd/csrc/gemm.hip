@@ -599,8 +599,9 @@ __global__ __launch_bounds__(256, 3) void gemm_ln_rows_kernel(GemmArgs p, LnArgs
 // the 16 rows.  KS = 1: the workgroup spans 384 columns (with LN it applies the
 // LayerNorm + SmoothQuant of `ln` to its 16 output rows, reference
 // src/simd_math.rs:208-247, and p.out is not written); KS = 2: 192 columns;
-// KS = 8: long K, 48 columns (a workgroup streams an eighth of the weights of
-// the KS = 1 form).
+// KS = 8: 48 columns (a workgroup streams an eighth of the weights of the
+// KS = 1 form), for long K and for a LayerNorm prologue (four times the
+// workgroups of KS = 2, each normalizing its 16 rows).
 // ---------------------------------------------------------------------------
 constexpr int kSmallMaxK = 1536;
 constexpr int kSmallPitch = kSmallMaxK + 16;  // LDS bytes per A row: conflict-free fragment reads
@@ -1135,11 +1136,11 @@ bool gemm_small_path(int m) { return m > 0 && m <= kSmallM; }
 
 void launch_gemm_ln_prologue(const GemmArgs& p, const LnArgs& ln, int emode, hipStream_t st) {
   if (p.M <= 0 || p.M > kSmallM || p.K != 384) return;
-  const dim3 grid(((p.M + 15) / 16) * (p.N / 192));
+  const dim3 grid(((p.M + 15) / 16) * (p.N / 48));
   if (emode == kEpiGelu)
-    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, false, 2>), grid, dim3(512), 0, st, p, ln, PreArgs{});
+    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiGelu, false, 8>), grid, dim3(512), 0, st, p, ln, PreArgs{});
   else
-    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, false, 2>), grid, dim3(512), 0, st, p, ln, PreArgs{});
+    hipLaunchKernelGGL((gemm_small_kernel<kALn, kEpiF32, false, 8>), grid, dim3(512), 0, st, p, ln, PreArgs{});
 }
 
 void launch_gemm_pre_ln(const GemmArgs& p, const PreArgs& pre, const LnArgs& ln, int emode, hipStream_t st) {
