@@ -200,9 +200,9 @@ int ae_attention_varlen_quantized(const float* qkv_dev, const int32_t* cu_seqlen
  * host and does not synchronize: the caller states max_seq_len (1..512), every
  * segment must hold 1..max_seq_len tokens (rows of a longer one are
  * unspecified).  The only scratch, the tile plan, is a static device array of
- * 131072 records (2 MiB, held by each GPU the library runs on until the process
- * ends; two lists of tiles): total_tokens / 32 + n_seqs + 2 <= 65536, else
- * AE_ERR_CAPACITY.  All
+ * 524288 records (8 MiB, held by each GPU the library runs on until the process
+ * ends; two lists of 4 + 12 (total_tokens / 32 + n_seqs + 1) records):
+ * total_tokens / 32 + n_seqs + 1 <= 21845, else AE_ERR_CAPACITY.  All
  * calls on one GPU share that array, so calls that overlap on one GPU race.
  * The first call on a device (current) resolves the array's address there and
  * must not be inside a stream capture. */

@@ -34,52 +34,138 @@ constexpr int kAttnQ = 32;     // queries per workgroup
 // keys, 53.8 KB, C3 ran 6 % slower, as with two workgroups per CU.)
 constexpr int kAttnLongL = 400;
 
-// Work plan, built on the device from cu_seqlens: one 16-byte record per tile
-// of kAttnQ queries, {s0, L, q0, nq} = the segment's first token, its length,
-// the tile's first query and its number of queries, so a workgroup learns its
-// whole assignment from one scalar load.  Tiles follow the packed segment order
-// (neighbouring tiles read neighbouring K/V rows).  A plan holds two lists of
-// max_tiles + 1 records each: the tiles in records 0 .. n - 1 and n in record
-// max_tiles (.x).  split = 0: every tile in list 0; split = 1: rows of at most
-// kAttnLongL keys in list 0, longer rows in list 1.  Rows past lmax (the score
-// row length) get no tiles, and a list holds at most max_tiles tiles (a
-// cu_seqlens that is not a prefix sum of at most T tokens could ask for more).
+// Work plan, built on the device from cu_seqlens (attention_plan_kernel).  An
+// item is kAttnQ queries of one segment and one head; its 16-byte record is
+// {s0, L, q0 | h << 16, nq}: the segment's first token, its length, the first
+// query, the head and the number of queries, so a workgroup learns its whole
+// assignment from two scalar loads (plan_item).  The hardware deals a launch's
+// workgroups to the 8 XCDs round-robin (workgroup p to XCD p % 8), so the plan
+// gives each XCD a list of its own, which its workgroups x, x + 8, x + 16, ...
+// take in order.  The items of one (segment, head), which share its K and V
+// rows, are dealt together: they run on one XCD and hit in its L2.  Groups are
+// dealt longest first (by tile count), one per XCD per round, in snake order
+// (rounds alternate XCDs 0..7 and 7..0), so every XCD runs its longest tiles
+// first and ends on short ones.  An XCD receives at most the average plus one
+// group (16 items at 512 keys): each of its groups is at most its round's
+// first, and the average is at least the sum of the full rounds' last groups,
+// which telescopes (attention_plan_cap).
+//
+// A plan holds two lists of kPlanHdr + 12 max_tiles records: int2 x of records
+// 0..3 is XCD x's (item count, first item), the items follow.  split = 0: every
+// row in list 0; split = 1: rows of at most kAttnLongL keys in list 0, longer
+// rows in list 1.  Rows are clamped to lmax keys (the score row length).  A list
+// whose segments would need more than max_tiles tiles (cu_seqlens not a prefix
+// sum of at most T tokens) gets no items.
+constexpr int kPlanBuckets = 17;  // tiles per segment 0..16 (rows of at most 512 keys)
+
 __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int B, int lmax, int max_tiles, int split,
                                                              int4* plan) {
-  __shared__ int part[2][256];
+  // cnt[l][n][t]: thread t's segments of list l with n tiles, then their
+  // exclusive prefix over the threads (the ranks of thread t's first ones)
+  __shared__ int cnt[2][kPlanBuckets][256];
+  // part[l][x][t]: items of XCD x in thread t's chunk of rounds, then the
+  // exclusive prefix over the chunks
+  __shared__ int part[2][8][256];
+  __shared__ int tot[2][kPlanBuckets], first[2][kPlanBuckets], xoff[2][8], bad[2];
   const int tid = threadIdx.x;
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
+  const int lcap = min(lmax, 16 * kAttnQ);
+  auto seg_len = [&](int b) { return max(0, min(cu[b + 1] - cu[b], lcap)); };
   auto list_of = [&](int L) { return split && L > kAttnLongL ? 1 : 0; };
-  int nt[2] = {0, 0};
-  for (int b = b0; b < b1; b++) {
-    const int L = min(cu[b + 1] - cu[b], lmax);
-    nt[list_of(L)] += (L + kAttnQ - 1) / kAttnQ;
+  for (int l = 0; l < 2; l++) {
+    for (int n = 0; n < kPlanBuckets; n++) cnt[l][n][tid] = 0;
+    for (int x = 0; x < 8; x++) part[l][x][tid] = 0;
   }
-  part[0][tid] = nt[0];
-  part[1][tid] = nt[1];
+  for (int b = b0; b < b1; b++) {
+    const int L = seg_len(b);
+    cnt[list_of(L)][(L + kAttnQ - 1) / kAttnQ][tid]++;
+  }
   __syncthreads();
-  if (tid < 2) {  // exclusive prefix sums; part[l][0] ends as list l's total (slot 0's prefix is 0)
+  if (tid < 2 * kPlanBuckets) {
+    int* c = cnt[tid / kPlanBuckets][tid % kPlanBuckets];
     int acc = 0;
     for (int i = 0; i < 256; i++) {
-      const int v = part[tid][i];
-      part[tid][i] = acc;
+      const int v = c[i];
+      c[i] = acc;
       acc += v;
     }
-    part[tid][0] = acc;
+    tot[tid / kPlanBuckets][tid % kPlanBuckets] = acc;
   }
   __syncthreads();
-  int at[2] = {tid == 0 ? 0 : part[0][tid], tid == 0 ? 0 : part[1][tid]};
-  int4* lst[2] = {plan, plan + max_tiles + 1};
-  const int n[2] = {min(part[0][0], max_tiles), min(part[1][0], max_tiles)};
-  for (int b = b0; b < b1; b++) {
-    const int s0 = cu[b], L = min(cu[b + 1] - s0, lmax), l = list_of(L);
-    for (int q0 = 0; q0 < L; q0 += kAttnQ, at[l]++)
-      if (at[l] < n[l]) lst[l][at[l]] = make_int4(s0, L, q0, min(kAttnQ, L - q0));
+  if (tid < 2) {  // first rank of each tile count, longest first; first[l][0] = segments with tiles
+    int acc = 0;
+    for (int n = kPlanBuckets - 1; n >= 1; n--) {
+      first[tid][n] = acc;
+      acc += tot[tid][n];
+    }
+    first[tid][0] = acc;
   }
-  if (tid == 0) {
-    lst[0][max_tiles] = make_int4(n[0], 0, 0, 0);
-    lst[1][max_tiles] = make_int4(n[1], 0, 0, 0);
+  __syncthreads();
+  // tile count of the segment of rank r < first[l][0] in list l
+  auto tiles_of_rank = [&](int l, int r) {
+    int n = kPlanBuckets - 1;
+    while (n > 1 && r >= first[l][n] + tot[l][n]) n--;
+    return n;
+  };
+  int G[2], RC[2];  // groups (segment, head) and rounds per thread chunk
+  for (int l = 0; l < 2; l++) {
+    G[l] = 12 * first[l][0];
+    RC[l] = (((G[l] + 7) >> 3) + 255) / 256;
+    const int j1 = min((G[l] + 7) >> 3, (tid + 1) * RC[l]);
+    for (int j = tid * RC[l]; j < j1; j++)
+      for (int pos = 0; pos < 8; pos++) {
+        const int k = 8 * j + pos;
+        if (k < G[l]) part[l][(j & 1) ? 7 - pos : pos][tid] += tiles_of_rank(l, k / 12);
+      }
+  }
+  __syncthreads();
+  if (tid < 16) {
+    int* c = part[tid >> 3][tid & 7];
+    int acc = 0;
+    for (int i = 0; i < 256; i++) {
+      const int v = c[i];
+      c[i] = acc;
+      acc += v;
+    }
+    xoff[tid >> 3][tid & 7] = acc;  // XCD x's item count, made its first item below
+  }
+  __syncthreads();
+  const size_t list_records = kPlanHdr + 12 * (size_t)max_tiles;
+  if (tid < 2) {
+    const int l = tid;
+    int tiles = 0;
+    for (int n = 1; n < kPlanBuckets; n++) tiles += n * tot[l][n];
+    bool ok = tiles <= max_tiles;
+    for (int x = 0; x < 8; x++) ok = ok && xoff[l][x] <= attention_plan_cap(max_tiles);
+    bad[l] = ok ? 0 : 1;
+    int2* hdr = reinterpret_cast<int2*>(plan + l * list_records);
+    int acc = 0;
+    for (int x = 0; x < 8; x++) {
+      const int c = xoff[l][x];
+      hdr[x] = make_int2(ok ? c : 0, acc);
+      xoff[l][x] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+  for (int b = b0; b < b1; b++) {
+    const int s0 = cu[b], L = seg_len(b), l = list_of(L), n = (L + kAttnQ - 1) / kAttnQ;
+    if (n == 0) continue;
+    const int rank = first[l][n] + cnt[l][n][tid]++;
+    if (bad[l]) continue;
+    int4* items = plan + l * list_records + kPlanHdr;
+    for (int h = 0; h < 12; h++) {
+      const int k = 12 * rank + h, j = k >> 3, pos = k & 7, x = (j & 1) ? 7 - pos : pos;
+      const int c = j / RC[l];  // the thread chunk that counted round j
+      int off = xoff[l][x] + part[l][x][c];
+      for (int jj = c * RC[l]; jj < j; jj++) {  // XCD x's groups in the chunk's earlier rounds
+        const int kk = 8 * jj + ((jj & 1) ? 7 - x : x);
+        if (kk < G[l]) off += tiles_of_rank(l, kk / 12);
+      }
+      for (int t = 0; t < n; t++)
+        items[off + t] = make_int4(s0, L, (t * kAttnQ) | (h << 16), min(kAttnQ, L - t * kAttnQ));
+    }
   }
 }
 
@@ -121,10 +207,10 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 
 // dynamic LDS: S[kAttnQ][pitch] scores -> exps, per tile: pitch = round16(L) + 4
 // (at most the launch's s_pitch, or kAttnLongL + 4 in the short-row launch)
-// The tiles of one (sequence, head) share that head's K and V: with the
-// XCD-contiguous numbering they run on one XCD and hit in its L2.
-// grid: max_tiles * 12 workgroups (a bound); the plan's n tiles give 12 n
-// logical items, numbered by plan_item (the surplus workgroups leave at once)
+// The tiles of one (sequence, head) share that head's K and V: the plan deals
+// them to one XCD, where they hit in its L2.
+// grid: 8 attention_plan_cap(max_tiles) workgroups (a bound); plan_item maps
+// them to the plan's items (the surplus workgroups leave at once)
 //
 // kWide: operands in float4 groups with four MFMA results live at a time (one
 // float4 load of K per 16 dims, one float4 LDS read of P per 16 keys, and four
@@ -132,14 +218,13 @@ __device__ __forceinline__ void add_blocks(float (&acc)[4], const v16f& pr) {
 // at a time with scalar operands, 92 VGPRs: for short rows, where the score
 // tile leaves room for more waves than the wide variant's registers do.
 template <bool kWide>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int max_tiles, int list) {
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p, int list_records, int list) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kAttnQ];
   __shared__ float s_max[kAttnQ], s_inv[kAttnQ];
-  int h, tile;
-  const int4* plan = reinterpret_cast<const int4*>(p.plan) + (size_t)list * (max_tiles + 1);
-  if (!plan_item(plan, max_tiles, h, tile)) return;  // a surplus workgroup
-  const int4 rec = plan[tile];
+  int h;
+  int4 rec;
+  if (!plan_item(reinterpret_cast<const int4*>(p.plan) + (size_t)list * list_records, h, rec)) return;  // surplus
   const int nq = rec.w;
   if (nq == 0) return;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;  // L <= s_pitch - 4 (the plan clamps it)
@@ -992,11 +1077,13 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
   const int max_tiles = attention_max_tiles(p.B, T);
   if (plan) launch_attention_plan(p, st, split ? 1 : 0, max_tiles);
   const bool wide = T > kWideMinMeanLen * p.B;
+  const int records = (int)attention_plan_list_records(p.B, T);
+  const dim3 grid(8 * attention_plan_cap(max_tiles));
   auto launch = [&](int list, size_t lds) {
     if (wide)
-      hipLaunchKernelGGL(attention_kernel<true>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, list);
+      hipLaunchKernelGGL(attention_kernel<true>, grid, dim3(256), lds, st, p, records, list);
     else
-      hipLaunchKernelGGL(attention_kernel<false>, dim3(max_tiles * 12), dim3(256), lds, st, p, max_tiles, list);
+      hipLaunchKernelGGL(attention_kernel<false>, grid, dim3(256), lds, st, p, records, list);
   };
   if (split) {
     launch(0, attention_lds_bytes(kAttnLongL + 4));
@@ -1015,7 +1102,7 @@ void launch_attention(const AttnArgs& p, int T, hipStream_t st, bool plan) {
 // shares that GPU's array: calls that overlap on one GPU race.  The plan kernel
 // rewrites every record a launch reads, so nothing needs clearing between calls.
 // ---------------------------------------------------------------------------
-static __device__ __align__(256) int4 scratch[kNoAllocPlanTiles];
+static __device__ __align__(256) int4 scratch[kNoAllocPlanRecords];
 
 namespace {
 constexpr int kNoAllocMaxDevices = 64;

@@ -165,14 +165,14 @@ __global__ __launch_bounds__(256) void sme_vquant_kernel(const float* qkv, const
 // One workgroup per (head, tile of 32 queries of one segment), the exact
 // kernel's tile records and numbering (plan_item).  The only LDS tile is the
 // int16 P[32][pitch16] (33 KB at 512 keys): several workgroups per CU.
-__global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, int max_tiles, size_t vt_len) {
+__global__ __launch_bounds__(256) void sme_attention_kernel(AttnArgs p, SmeArgs sa, size_t vt_len) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   __shared__ float s_maxw[4][kSmeQ];
   __shared__ float s_max[kSmeQ], s_pscale[kSmeQ], s_vscale[32];
   __shared__ int s_isum[kSmeQ];
-  int h, tile;
-  if (!plan_item(reinterpret_cast<const int4*>(p.plan), max_tiles, h, tile)) return;  // a surplus workgroup
-  const int4 rec = reinterpret_cast<const int4*>(p.plan)[tile];
+  int h;
+  int4 rec;
+  if (!plan_item(reinterpret_cast<const int4*>(p.plan), h, rec)) return;  // a surplus workgroup (list 0)
   const int nq = rec.w;
   const int s0 = rec.x, L = rec.y, q0 = rec.z;
   // per_seq: sequences under 16 tokens take the exact attention (forward_cls,
@@ -397,8 +397,8 @@ void launch_attention_sme(const AttnArgs& p, const SmeArgs& s, int T, hipStream_
   hipLaunchKernelGGL(sme_vquant_kernel, dim3((T + 63) / 64, 12), dim3(256), 0, st, p.qkv, p.cu, p.B, T, s, vt_len);
   const int max_tiles = attention_max_tiles(p.B, T);
   if (plan) launch_attention_plan(p, st, 0, max_tiles);  // every tile in list 0
-  hipLaunchKernelGGL(sme_attention_kernel, dim3(max_tiles * 12), dim3(256), sme_p_bytes(p.s_pitch), st, p, s,
-                     max_tiles, vt_len);
+  hipLaunchKernelGGL(sme_attention_kernel, dim3(8 * attention_plan_cap(max_tiles)), dim3(256), sme_p_bytes(p.s_pitch),
+                     st, p, s, vt_len);
 }
 
 void init_attention_sme_kernels() {

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernels.hpp"  // kPlanHdr
+
 namespace aek {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -256,20 +258,19 @@ __device__ __forceinline__ int xcd_contiguous(int p, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
 }
 
-// The attention kernels' workgroup numbering over a tile plan whose record
-// max_tiles holds the number n of real tiles (attention_plan_kernel): the 12 n
-// (head, tile) items, item = head * n + tile, are numbered XCD-contiguously over
-// the workgroups the hardware dispatches first (XCD x = id mod 8 takes one
-// contiguous range of items in its dispatch order), so the surplus workgroups of
-// the worst-case grid come last on every XCD.  False for those.
-__device__ __forceinline__ bool plan_item(const int4* plan, int max_tiles, int& h, int& tile) {
-  const int n = plan[max_tiles].x;
-  const int nitems = 12 * n, q = nitems >> 3, r = nitems & 7;
-  const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
-  if (i >= (x < r ? q + 1 : q)) return false;
-  const int item = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
-  h = item / n;
-  tile = item - h * n;
+// The attention kernels' workgroup -> item map over one list of a tile plan
+// (attention_plan_kernel): workgroup p runs on XCD x = p mod 8 (the hardware's
+// round-robin dispatch) and takes item p / 8 of XCD x's list, whose count and
+// first item are int2 x of the list's header.  The surplus workgroups of the
+// worst-case grid come last on every XCD and leave after the header load:
+// false for those.  rec = {s0, L, q0, nq}.
+__device__ __forceinline__ bool plan_item(const int4* list, int& h, int4& rec) {
+  const int2 hx = reinterpret_cast<const int2*>(list)[blockIdx.x & 7];
+  const int i = blockIdx.x >> 3;
+  if (i >= hx.x) return false;
+  rec = list[kPlanHdr + hx.y + i];
+  h = rec.z >> 16;
+  rec.z &= 0xffff;
   return true;
 }
 

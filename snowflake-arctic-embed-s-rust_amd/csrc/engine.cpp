@@ -1084,11 +1084,11 @@ int ae_attention_varlen_noalloc(const float* qkv_dev, const int32_t* cu_seqlens_
       max_seq_len > ae::kMaxPos)
     return fail(AE_ERR_INVALID_ARG, "bad attention arguments (max_seq_len must be 1..512)");
   if (n_seqs == 0) return AE_OK;
-  if (2 * (aek::attention_max_tiles(n_seqs, total_tokens) + 1) > aek::kNoAllocPlanTiles)
-    return fail(AE_ERR_CAPACITY, "ae_attention_varlen_noalloc: 2 (total_tokens / 32 + n_seqs + 2) = " +
-                                     std::to_string(2 * (aek::attention_max_tiles(n_seqs, total_tokens) + 1)) +
-                                     " exceeds its static scratch of " + std::to_string(aek::kNoAllocPlanTiles) +
-                                     " tiles");
+  const size_t records = 2 * aek::attention_plan_list_records(n_seqs, total_tokens);
+  if (records > (size_t)aek::kNoAllocPlanRecords)
+    return fail(AE_ERR_CAPACITY, "ae_attention_varlen_noalloc: 2 (4 + 12 (total_tokens / 32 + n_seqs + 1)) = " +
+                                     std::to_string(records) + " plan records exceed its static scratch of " +
+                                     std::to_string(aek::kNoAllocPlanRecords));
   int* plan = nullptr;
   const hipError_t e = aek::noalloc_plan_scratch(&plan);
   if (e != hipSuccess) return fail(AE_ERR_HIP, std::string("no-allocation attention scratch: ") + hipGetErrorString(e));

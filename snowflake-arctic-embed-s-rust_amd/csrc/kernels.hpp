@@ -156,13 +156,19 @@ int attention_pitch(int max_len);
 size_t attention_lds_bytes(int s_pitch);
 // tiles of 32 queries: max_tiles >= sum_b ceil(L_b / 32); T/32 + B + 1 is one
 inline int attention_max_tiles(int B, int T) { return T / 32 + B + 1; }
-// ints of `plan` scratch for B segments and T tokens: two lists of one 4-int
-// record per tile and one for the list's tile count
-inline size_t attention_plan_ints(int B, int T) { return 8 * ((size_t)attention_max_tiles(B, T) + 1); }
+// a plan list: kPlanHdr header records (each XCD's item count and first item),
+// then one 4-int record per (tile, head)
+constexpr int kPlanHdr = 4;
+inline size_t attention_plan_list_records(int B, int T) { return kPlanHdr + 12 * (size_t)attention_max_tiles(B, T); }
+// ints of `plan` scratch for B segments and T tokens: two lists
+inline size_t attention_plan_ints(int B, int T) { return 8 * attention_plan_list_records(B, T); }
+// items of one list on one XCD: at most the average (12 max_tiles / 8) plus one
+// (segment, head) group of up to 16 tiles; a launch runs 8 times this many workgroups
+constexpr int attention_plan_cap(int max_tiles) { return (12 * max_tiles + 7) / 8 + 16; }
 void init_attention_kernels();  // once per device before the first launch (not during capture)
 // ae_attention_varlen_noalloc: the tile plan in a static device array of this
-// many records (2 MiB), so 2 (attention_max_tiles(B, T) + 1) <= kNoAllocPlanTiles
-constexpr int kNoAllocPlanTiles = 131072;
+// many records (8 MiB), so 2 attention_plan_list_records(B, T) <= kNoAllocPlanRecords
+constexpr int kNoAllocPlanRecords = 524288;
 // the current device's address of that array (resolved on the first call per
 // device, with the device current; not during a stream capture)
 hipError_t noalloc_plan_scratch(int** plan);

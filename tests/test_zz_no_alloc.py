@@ -37,7 +37,7 @@ def test_noalloc_attention_matches_allocating_operator(torch_gpu):
         r, o = ref.cpu().numpy(), out.cpu().numpy()
         assert np.all(np.isfinite(r))
         assert np.array_equal(r.view(np.uint32), o.view(np.uint32)), lens
-    # past the static scratch (131072 tile records, two lists): refused before any launch
+    # past the static scratch (524288 plan records, two lists): refused before any launch
     assert _call(lib, 1, 1, 60000, 1 << 20, 512, 1) == ae.AE_ERR_CAPACITY
     assert "static scratch" in ae.lib().ae_last_error().decode()
     assert _call(lib, 1, 1, 2, 100, 513, 1) == ae.AE_ERR_INVALID_ARG
