@@ -62,12 +62,27 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
                                                              int4* plan) {
   // cnt[l][n][t]: thread t's segments of list l with n tiles, then their
   // exclusive prefix over the threads (the ranks of thread t's first ones)
-  __shared__ int cnt[2][kPlanBuckets][256];
+  __shared__ __attribute__((aligned(16))) int cnt[2][kPlanBuckets][256];
   // part[l][x][t]: items of XCD x in thread t's chunk of rounds, then the
   // exclusive prefix over the chunks
-  __shared__ int part[2][8][256];
+  __shared__ __attribute__((aligned(16))) int part[2][8][256];
   __shared__ int tot[2][kPlanBuckets], first[2][kPlanBuckets], xoff[2][8], bad[2];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // exclusive prefix sum of a 256-int LDS row, by one whole wave (4 entries per
+  // lane, then a shuffle scan over the lanes); *total gets the row's sum
+  auto scan_row = [&](int* row, int* total) {
+    const int4 v = reinterpret_cast<const int4*>(row)[lane];
+    const int sum = v.x + v.y + v.z + v.w;
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    const int ex = incl - sum;
+    reinterpret_cast<int4*>(row)[lane] = make_int4(ex, ex + v.x, ex + v.x + v.y, ex + v.x + v.y + v.z);
+    if (lane == 63) *total = incl;
+  };
   const int per = (B + 255) / 256;
   const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
   const int lcap = min(lmax, 16 * kAttnQ);
@@ -82,16 +97,8 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
     cnt[list_of(L)][(L + kAttnQ - 1) / kAttnQ][tid]++;
   }
   __syncthreads();
-  if (tid < 2 * kPlanBuckets) {
-    int* c = cnt[tid / kPlanBuckets][tid % kPlanBuckets];
-    int acc = 0;
-    for (int i = 0; i < 256; i++) {
-      const int v = c[i];
-      c[i] = acc;
-      acc += v;
-    }
-    tot[tid / kPlanBuckets][tid % kPlanBuckets] = acc;
-  }
+  for (int r = wave; r < 2 * kPlanBuckets; r += 4)  // wave-uniform
+    scan_row(cnt[r / kPlanBuckets][r % kPlanBuckets], &tot[r / kPlanBuckets][r % kPlanBuckets]);
   __syncthreads();
   if (tid < 2) {  // first rank of each tile count, longest first; first[l][0] = segments with tiles
     int acc = 0;
@@ -102,13 +109,22 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
     first[tid][0] = acc;
   }
   __syncthreads();
-  // tile count of the segment of rank r < first[l][0] in list l
+  // tile count of the segment of rank r < first[l][0] in list l: 1 + the
+  // number of buckets n >= 2 whose ranks end after r (ranks run longest first),
+  // from the bucket ends held in registers
+  int bend[2][kPlanBuckets - 2];
+#pragma unroll
+  for (int l = 0; l < 2; l++)
+#pragma unroll
+    for (int m = 0; m < kPlanBuckets - 2; m++) bend[l][m] = first[l][m + 2] + tot[l][m + 2];
   auto tiles_of_rank = [&](int l, int r) {
-    int n = kPlanBuckets - 1;
-    while (n > 1 && r >= first[l][n] + tot[l][n]) n--;
+    int n = 1;
+#pragma unroll
+    for (int m = 0; m < kPlanBuckets - 2; m++) n += r < (l ? bend[1][m] : bend[0][m]) ? 1 : 0;
     return n;
   };
   int G[2], RC[2];  // groups (segment, head) and rounds per thread chunk
+#pragma unroll
   for (int l = 0; l < 2; l++) {
     G[l] = 12 * first[l][0];
     RC[l] = (((G[l] + 7) >> 3) + 255) / 256;
@@ -120,16 +136,7 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
       }
   }
   __syncthreads();
-  if (tid < 16) {
-    int* c = part[tid >> 3][tid & 7];
-    int acc = 0;
-    for (int i = 0; i < 256; i++) {
-      const int v = c[i];
-      c[i] = acc;
-      acc += v;
-    }
-    xoff[tid >> 3][tid & 7] = acc;  // XCD x's item count, made its first item below
-  }
+  for (int r = wave; r < 16; r += 4) scan_row(part[r >> 3][r & 7], &xoff[r >> 3][r & 7]);  // XCD counts, then firsts
   __syncthreads();
   const size_t list_records = kPlanHdr + 12 * (size_t)max_tiles;
   if (tid < 2) {
@@ -154,14 +161,15 @@ __global__ __launch_bounds__(256) void attention_plan_kernel(const int* cu, int 
     if (n == 0) continue;
     const int rank = first[l][n] + cnt[l][n][tid]++;
     if (bad[l]) continue;
+    const int Gl = l ? G[1] : G[0], RCl = l ? RC[1] : RC[0];  // (static register indexes)
     int4* items = plan + l * list_records + kPlanHdr;
     for (int h = 0; h < 12; h++) {
       const int k = 12 * rank + h, j = k >> 3, pos = k & 7, x = (j & 1) ? 7 - pos : pos;
-      const int c = j / RC[l];  // the thread chunk that counted round j
+      const int c = j / RCl;  // the thread chunk that counted round j
       int off = xoff[l][x] + part[l][x][c];
-      for (int jj = c * RC[l]; jj < j; jj++) {  // XCD x's groups in the chunk's earlier rounds
+      for (int jj = c * RCl; jj < j; jj++) {  // XCD x's groups in the chunk's earlier rounds
         const int kk = 8 * jj + ((jj & 1) ? 7 - x : x);
-        if (kk < G[l]) off += tiles_of_rank(l, kk / 12);
+        if (kk < Gl) off += tiles_of_rank(l, kk / 12);
       }
       for (int t = 0; t < n; t++)
         items[off + t] = make_int4(s0, L, (t * kAttnQ) | (h << 16), min(kAttnQ, L - t * kAttnQ));
